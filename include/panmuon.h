@@ -1,0 +1,220 @@
+/*
+ * panmuon.h — C ABI of the MI355X (gfx950) Muon optimizer library, libpanmuon.so.
+ *
+ * The library replaces the device work behind PAN 2's patched Muon step:
+ *   - the per-parameter loop of pan/optim/patch_muon.py:146-171
+ *     (momentum -> Newton–Schulz -> parameter step), and
+ *   - the Triton/quack kernels it calls (pan/optim/muon_triton.py,
+ *     quack gemm_symmetric, gemm_symmetric_out and gemm_out at pan/optim/patch_muon.py:310-333).
+ *
+ * Conventions (mirroring the reference):
+ *   - Parameters and momentum buffers belong to the caller and are updated in
+ *     place; every other buffer lives in a caller-provided device workspace.
+ *     No entry point allocates device memory.
+ *   - All device work is enqueued on the caller's stream (a hipStream_t passed
+ *     as void*); nothing synchronises the host.
+ *   - Return codes: 0 on success, a negative PM_E* value on failure; the text
+ *     of the last failure on the calling thread is pm_last_error().
+ *   - Matrices are row-major with unit column stride and a row stride ("ld")
+ *     in elements.
+ *
+ * Newton–Schulz is the standard quintic of torch.optim._muon
+ * (_zeropower_via_newtonschulz, torch/optim/_muon.py:31-70): per iteration
+ * A = X Xᵀ, B = b A + c A², X <- a X + B X, with X oriented so that its short
+ * side is contracted. Operands are bf16, accumulation fp32, and every GEMM
+ * output is rounded to bf16 exactly where torch rounds it.
+ */
+#ifndef PANMUON_H
+#define PANMUON_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PM_ABI_VERSION 1
+
+/* Element types accepted for params, grads, momentum buffers and updates. */
+enum pm_dtype {
+  PM_DTYPE_F32 = 0,
+  PM_DTYPE_BF16 = 1
+};
+
+enum pm_status {
+  PM_OK = 0,
+  PM_EINVAL = -1,       /* bad argument (null pointer, bad shape, bad stride) */
+  PM_EDTYPE = -2,       /* unsupported dtype */
+  PM_EWORKSPACE = -3,   /* workspace too small */
+  PM_EHIP = -4,         /* a HIP runtime call failed */
+  PM_EUNSUPPORTED = -5  /* valid request this build does not implement */
+};
+
+/*
+ * One Muon parameter (a 2-D weight, or one row block of a chunked weight).
+ * param/grad/momentum are rows x cols with their own row strides.
+ * adj_ratio is the shape factor of torch.optim._muon._adjust_lr
+ * (torch/optim/_muon.py:73-84): adjusted_lr = lr * adj_ratio. It is computed
+ * by the caller from the shape the reference passes (the chunk shape for
+ * chunked params, pan/optim/patch_muon.py:142).
+ */
+typedef struct pm_matrix {
+  void* param;
+  const void* grad;
+  void* momentum;
+  int64_t rows;
+  int64_t cols;
+  int64_t param_ld;
+  int64_t grad_ld;
+  int64_t momentum_ld;
+  int32_t param_dtype;
+  int32_t grad_dtype;
+  int32_t momentum_dtype;
+  int32_t reserved;
+  double adj_ratio;
+} pm_matrix;
+
+/* One matrix for the Newton–Schulz-only entry point: out = NS(in), bf16. */
+typedef struct pm_ns_matrix {
+  const void* in;
+  void* out;
+  int64_t rows;
+  int64_t cols;
+  int64_t in_ld;
+  int64_t out_ld;
+  int32_t in_dtype;
+  int32_t reserved;
+} pm_ns_matrix;
+
+/*
+ * Hyper-parameters shared by every matrix of one call. They are the keyword
+ * arguments of torch.optim._muon._single_tensor_muon
+ * (pan/optim/patch_muon.py:44-58): momentum, nesterov, ns_coefficients,
+ * ns_steps, eps, weight_decay.
+ *   coeffs: NULL to use (a, b, c) for every iteration, or a host array of
+ *           ns_steps triples (a, b, c) — one per iteration.
+ *   workspace_limit: upper bound in bytes on the workspace pm_workspace_bytes
+ *           asks for (0 = library default); matrices are then processed in
+ *           groups that fit.
+ */
+typedef struct pm_hparams {
+  float momentum;
+  int32_t nesterov;
+  int32_t ns_steps;
+  float eps;
+  double weight_decay;
+  float a;
+  float b;
+  float c;
+  const float* coeffs;
+  uint64_t workspace_limit;
+} pm_hparams;
+
+/* ABI version of the loaded library (PM_ABI_VERSION). */
+int pm_abi_version(void);
+
+/* Text of the last failure on the calling thread ("" if none). */
+const char* pm_last_error(void);
+
+/*
+ * Workspace needed by pm_muon_step for these matrices. Replaces the torch
+ * caching-allocator temporaries of pan/optim/muon_triton.py:98 and
+ * pan/optim/patch_muon.py:305-308. Returns 0 and sets pm_last_error on a bad
+ * argument.
+ */
+size_t pm_workspace_bytes(const pm_matrix* mats, int n, const pm_hparams* hp);
+
+/*
+ * One Muon step over n matrices, in place. Replaces the single-GPU per-param
+ * loop of PAN 2's _single_tensor_muon (pan/optim/patch_muon.py:146-171):
+ *   buf <- mu*buf + (1-mu)*g;  u <- (1-mu)*g + mu*buf   (nesterov; else u = buf)
+ *                                    (pan/optim/muon_triton.py:44-48)
+ *   O   <- NS(u)                     (torch/optim/_muon.py:55-69)
+ *   p   <- p*(1 - lr*wd) - lr*adj_ratio*O
+ *                                    (pan/optim/muon_triton.py:130-131,188-190)
+ * lr is read from lr_dev (a device float, the reference's tensor lr path,
+ * pan/optim/muon_triton.py:152-159) when it is not NULL, else lr_host.
+ */
+int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp,
+                 const float* lr_dev, double lr_host,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by pm_newton_schulz. */
+size_t pm_ns_workspace_bytes(const pm_ns_matrix* mats, int n, const pm_hparams* hp);
+
+/*
+ * Newton–Schulz only: out_i = NS(in_i) in bf16, same shape as in_i.
+ * Replaces torch.optim._muon._zeropower_via_newtonschulz, which PAN 2's
+ * patch_muon swaps for _gram_newtonschulz_local (pan/optim/patch_muon.py:339).
+ */
+int pm_newton_schulz(const pm_ns_matrix* mats, int n, const pm_hparams* hp,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Fused Nesterov momentum over n contiguous elements. Replaces
+ * muon_momentum_nesterov (pan/optim/muon_triton.py:54-108): buf is updated in
+ * place and the update is written to `update` in update_dtype.
+ */
+int pm_momentum_nesterov(void* buf, int32_t buf_dtype,
+                         const void* grad, int32_t grad_dtype,
+                         void* update, int32_t update_dtype,
+                         int64_t n, float momentum, int32_t nesterov, void* stream);
+
+/*
+ * Fused parameter step over n contiguous elements. Replaces step_param
+ * (pan/optim/muon_triton.py:164-210): p <- p*(1 - lr*wd) - lr*adj_ratio*u,
+ * fp32 math; lr from lr_dev when it is not NULL, else lr_host.
+ */
+int pm_step_param(void* param, int32_t param_dtype,
+                  const void* update, int32_t update_dtype,
+                  int64_t n, const float* lr_dev, double lr_host,
+                  float weight_decay, double adj_ratio, void* stream);
+
+/*
+ * Symmetric gram C = X Xᵀ (bf16 in, fp32 accumulate, bf16 out) on the
+ * upper-triangle tiles, mirrored. Replaces quack gemm_symmetric_out(X, X.mT)
+ * (pan/optim/patch_muon.py:310). X is rows x cols with ld == cols, C is
+ * rows x rows with ld == rows; rows must be a multiple of 256 and cols a
+ * multiple of 64. Needs pm_gram_workspace_bytes() of workspace.
+ */
+size_t pm_gram_workspace_bytes(void);
+int pm_gram(const void* x, int64_t rows, int64_t cols, void* out,
+            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Opt-in launch timing (no counterpart in the reference, which has no
+ * instrumentation; used by bench.py for live roofline figures). While enabled,
+ * every launch of pm_muon_step / pm_newton_schulz records a HIP event on the
+ * call's stream; pm_timing_read waits for those events and returns one record
+ * per launch with its algorithmic work.
+ */
+enum pm_kernel_kind {
+  PM_K_PROLOGUE = 0,  /* momentum + bf16 X/Xᵀ + Σx² partials */
+  PM_K_NORM = 1,      /* per-matrix 1/‖X‖ */
+  PM_K_GRAM = 2,      /* A = X Xᵀ (symmetric) */
+  PM_K_POLY = 3,      /* B = b A + c A² (symmetric) */
+  PM_K_UPDATE = 4,    /* X <- a X + B X */
+  PM_K_FINAL = 5      /* last update fused with the parameter step */
+};
+
+typedef struct pm_launch_time {
+  int32_t kind;        /* pm_kernel_kind */
+  int32_t group;       /* workspace group within the call */
+  int32_t iteration;   /* Newton–Schulz iteration (-1 for prologue/norm) */
+  int32_t n_matrices;  /* matrices walked by this launch */
+  double flops;        /* algorithmic FLOPs (GEMM launches) */
+  double bytes;        /* algorithmic HBM bytes (prologue) */
+  float ms;            /* event-measured duration */
+  float reserved;
+} pm_launch_time;
+
+int pm_timing_enable(int on);
+/* Returns the number of records written (<= max) and clears them; < 0 on error. */
+int pm_timing_read(pm_launch_time* out, int max);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PANMUON_H */

@@ -1,0 +1,371 @@
+"""ctypes binding of libpanmuon.so (C ABI declared in include/panmuon.h).
+
+Every wrapper enqueues on torch's current stream of the tensors' device and
+never synchronises the host. There is no fallback: if the library is missing
+or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpanmuon.so")
+ABI_VERSION = 1
+
+PM_DTYPE_F32 = 0
+PM_DTYPE_BF16 = 1
+
+PM_EINVAL = -1
+PM_EDTYPE = -2
+PM_EWORKSPACE = -3
+PM_EHIP = -4
+PM_EUNSUPPORTED = -5
+
+# Every symbol the header declares (checked by tests/test_abi_exports.py).
+EXPORTS = (
+    "pm_abi_version",
+    "pm_last_error",
+    "pm_workspace_bytes",
+    "pm_muon_step",
+    "pm_ns_workspace_bytes",
+    "pm_newton_schulz",
+    "pm_momentum_nesterov",
+    "pm_step_param",
+    "pm_gram_workspace_bytes",
+    "pm_gram",
+    "pm_timing_enable",
+    "pm_timing_read",
+)
+
+KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final")
+
+
+class PmMatrix(ctypes.Structure):
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("momentum", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("param_ld", ctypes.c_int64),
+        ("grad_ld", ctypes.c_int64),
+        ("momentum_ld", ctypes.c_int64),
+        ("param_dtype", ctypes.c_int32),
+        ("grad_dtype", ctypes.c_int32),
+        ("momentum_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("adj_ratio", ctypes.c_double),
+    ]
+
+
+class PmNsMatrix(ctypes.Structure):
+    _fields_ = [
+        ("in_", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("in_ld", ctypes.c_int64),
+        ("out_ld", ctypes.c_int64),
+        ("in_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class PmHparams(ctypes.Structure):
+    _fields_ = [
+        ("momentum", ctypes.c_float),
+        ("nesterov", ctypes.c_int32),
+        ("ns_steps", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("weight_decay", ctypes.c_double),
+        ("a", ctypes.c_float),
+        ("b", ctypes.c_float),
+        ("c", ctypes.c_float),
+        ("coeffs", ctypes.POINTER(ctypes.c_float)),
+        ("workspace_limit", ctypes.c_uint64),
+    ]
+
+
+class PmLaunchTime(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("group", ctypes.c_int32),
+        ("iteration", ctypes.c_int32),
+        ("n_matrices", ctypes.c_int32),
+        ("flops", ctypes.c_double),
+        ("bytes", ctypes.c_double),
+        ("ms", ctypes.c_float),
+        ("reserved", ctypes.c_float),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libpanmuon.so once (after torch, so both share one HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m pan2_amd.build` (needs hipcc)")
+        lib = ctypes.CDLL(LIB_PATH)
+        vp, i32, i64, sz, f32, f64 = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                       ctypes.c_size_t, ctypes.c_float, ctypes.c_double)
+        pm, pns, php = ctypes.POINTER(PmMatrix), ctypes.POINTER(PmNsMatrix), ctypes.POINTER(PmHparams)
+        sig = {
+            "pm_abi_version": (ctypes.c_int, []),
+            "pm_last_error": (ctypes.c_char_p, []),
+            "pm_workspace_bytes": (sz, [pm, ctypes.c_int, php]),
+            "pm_muon_step": (ctypes.c_int, [pm, ctypes.c_int, php, vp, f64, vp, sz, vp]),
+            "pm_ns_workspace_bytes": (sz, [pns, ctypes.c_int, php]),
+            "pm_newton_schulz": (ctypes.c_int, [pns, ctypes.c_int, php, vp, sz, vp]),
+            "pm_momentum_nesterov": (ctypes.c_int, [vp, i32, vp, i32, vp, i32, i64, f32, i32, vp]),
+            "pm_step_param": (ctypes.c_int, [vp, i32, vp, i32, i64, vp, f64, f32, f64, vp]),
+            "pm_gram_workspace_bytes": (sz, []),
+            "pm_gram": (ctypes.c_int, [vp, i64, i64, vp, vp, sz, vp]),
+            "pm_timing_enable": (ctypes.c_int, [ctypes.c_int]),
+            "pm_timing_read": (ctypes.c_int, [ctypes.POINTER(PmLaunchTime), ctypes.c_int]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.pm_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"libpanmuon ABI {lib.pm_abi_version()} != expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().pm_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the reference's exception type for a failed call."""
+    if rc == 0:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc in (PM_EINVAL, PM_EDTYPE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return PM_DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return PM_DTYPE_BF16
+    raise TypeError(f"libpanmuon supports float32 and bfloat16 tensors, got {t.dtype}")
+
+
+def stream_of(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def make_hparams(*, momentum=0.95, nesterov=True, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5,
+                 eps=1e-7, weight_decay=0.0, workspace_limit=0):
+    """PmHparams plus the ctypes array that must outlive the call (per-step coefficients)."""
+    hp = PmHparams()
+    hp.momentum = float(momentum)
+    hp.nesterov = 1 if nesterov else 0
+    hp.ns_steps = int(ns_steps)
+    hp.eps = float(eps)
+    hp.weight_decay = float(weight_decay)
+    hp.workspace_limit = int(workspace_limit)
+    keep = None
+    coeffs = tuple(ns_coefficients)
+    if len(coeffs) == 3 and not isinstance(coeffs[0], (tuple, list)):
+        hp.a, hp.b, hp.c = (float(v) for v in coeffs)
+        hp.coeffs = None
+    else:
+        if len(coeffs) != ns_steps or any(len(t) != 3 for t in coeffs):
+            raise ValueError("ns_coefficients must be (a, b, c) or one (a, b, c) per step")
+        flat = [float(v) for t in coeffs for v in t]
+        keep = (ctypes.c_float * len(flat))(*flat)
+        hp.coeffs = ctypes.cast(keep, ctypes.POINTER(ctypes.c_float))
+        hp.a, hp.b, hp.c = flat[:3]
+    return hp, keep
+
+
+def _ld(t: torch.Tensor) -> int:
+    return t.stride(0)
+
+
+def _check_matrix(t: torch.Tensor, what: str) -> None:
+    if t.dim() != 2:
+        raise ValueError(f"{what} must be 2-D, got shape {tuple(t.shape)}")
+    if not t.is_cuda:
+        raise RuntimeError(f"{what} must be a HIP device tensor; libpanmuon has no CPU path")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        raise ValueError(f"{what} needs unit column stride and row stride >= cols")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, nesterov, ns_coefficients,
+              ns_steps, eps, workspace_limit: int = 0) -> None:
+    """pm_muon_step over matching lists of 2-D device tensors (updated in place).
+
+    lr: python float, or a 1-element float tensor on the same device (read on
+    the device, no host sync).
+    """
+    lib = load()
+    n = len(params)
+    if n == 0:
+        return
+    dev = params[0].device
+    mats = (PmMatrix * n)()
+    for i, (p, g, b, r) in enumerate(zip(params, grads, bufs, adj_ratios)):
+        _check_matrix(p, "param")
+        _check_matrix(g, "grad")
+        _check_matrix(b, "momentum buffer")
+        if p.shape != g.shape or p.shape != b.shape:
+            raise ValueError(f"param/grad/buffer shapes differ: {tuple(p.shape)}, {tuple(g.shape)}, {tuple(b.shape)}")
+        if p.device != dev or g.device != dev or b.device != dev:
+            raise ValueError("all tensors of one call must be on one device")
+        m = mats[i]
+        m.param, m.grad, m.momentum = p.data_ptr(), g.data_ptr(), b.data_ptr()
+        m.rows, m.cols = p.shape
+        m.param_ld, m.grad_ld, m.momentum_ld = _ld(p), _ld(g), _ld(b)
+        m.param_dtype, m.grad_dtype, m.momentum_dtype = dtype_code(p), dtype_code(g), dtype_code(b)
+        m.adj_ratio = float(r)
+    hp, keep = make_hparams(momentum=momentum, nesterov=nesterov, ns_coefficients=ns_coefficients,
+                            ns_steps=ns_steps, eps=eps, weight_decay=weight_decay,
+                            workspace_limit=workspace_limit)
+    lr_dev, lr_host, lr_keep = None, 0.0, None
+    if isinstance(lr, torch.Tensor):
+        if lr.numel() != 1:
+            raise ValueError("Tensor lr must be 1-element")
+        if lr.device.type == "cpu":
+            lr_host = float(lr.item())
+        else:
+            if lr.device != dev:
+                raise ValueError("lr tensor must be on the params' device")
+            lr_keep = lr.reshape(()).to(torch.float32)
+            lr_dev = lr_keep.data_ptr()
+    else:
+        lr_host = float(lr)
+    with torch.cuda.device(dev):
+        nbytes = lib.pm_workspace_bytes(mats, n, ctypes.byref(hp))
+        if nbytes == 0:
+            check(PM_EINVAL, "pm_workspace_bytes")
+        ws = workspace(nbytes, dev)
+        rc = lib.pm_muon_step(mats, n, ctypes.byref(hp), lr_dev, lr_host, ws.data_ptr(), nbytes, stream_of(dev))
+    check(rc, "pm_muon_step")
+    del keep, lr_keep
+
+
+def newton_schulz_into(pairs, *, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7,
+                       workspace_limit: int = 0) -> None:
+    """pm_newton_schulz over [(input, output)] pairs; outputs are bf16, same shape."""
+    lib = load()
+    n = len(pairs)
+    if n == 0:
+        return
+    dev = pairs[0][0].device
+    mats = (PmNsMatrix * n)()
+    for i, (x, o) in enumerate(pairs):
+        _check_matrix(x, "input")
+        _check_matrix(o, "output")
+        if o.dtype != torch.bfloat16 or o.shape != x.shape:
+            raise ValueError("output must be bf16 and shaped like the input")
+        m = mats[i]
+        m.in_, m.out = x.data_ptr(), o.data_ptr()
+        m.rows, m.cols = x.shape
+        m.in_ld, m.out_ld = _ld(x), _ld(o)
+        m.in_dtype = dtype_code(x)
+    hp, keep = make_hparams(ns_coefficients=ns_coefficients, ns_steps=ns_steps, eps=eps,
+                            workspace_limit=workspace_limit)
+    with torch.cuda.device(dev):
+        nbytes = lib.pm_ns_workspace_bytes(mats, n, ctypes.byref(hp))
+        if nbytes == 0:
+            check(PM_EINVAL, "pm_ns_workspace_bytes")
+        ws = workspace(nbytes, dev)
+        rc = lib.pm_newton_schulz(mats, n, ctypes.byref(hp), ws.data_ptr(), nbytes, stream_of(dev))
+    check(rc, "pm_newton_schulz")
+    del keep
+
+
+def momentum_nesterov_into(buf, grad, update, momentum: float, nesterov: bool = True) -> None:
+    lib = load()
+    for t, w in ((buf, "buf"), (grad, "grad"), (update, "update")):
+        if not t.is_cuda:
+            raise RuntimeError(f"{w} must be a HIP device tensor")
+        if not t.is_contiguous():
+            raise AssertionError(f"{w} must be contiguous")
+    if buf.shape != grad.shape or update.shape != grad.shape:
+        raise AssertionError("buf, grad and update must have the same shape")
+    with torch.cuda.device(buf.device):
+        rc = lib.pm_momentum_nesterov(buf.data_ptr(), dtype_code(buf), grad.data_ptr(), dtype_code(grad),
+                                      update.data_ptr(), dtype_code(update), buf.numel(), float(momentum),
+                                      1 if nesterov else 0, stream_of(buf.device))
+    check(rc, "pm_momentum_nesterov")
+
+
+def step_param_inplace(param, update, lr, weight_decay: float, adj_ratio: float) -> None:
+    lib = load()
+    for t, w in ((param, "param"), (update, "update")):
+        if not t.is_cuda:
+            raise RuntimeError(f"{w} must be a HIP device tensor")
+        if not t.is_contiguous():
+            raise AssertionError(f"{w} must be contiguous")
+    if param.shape != update.shape:
+        raise AssertionError("param and update must have the same shape")
+    lr_dev, lr_host, keep = None, 0.0, None
+    if isinstance(lr, torch.Tensor):
+        if lr.device.type == "cpu":
+            lr_host = float(lr.item())
+        else:
+            keep = lr.reshape(()).to(torch.float32)
+            lr_dev = keep.data_ptr()
+    else:
+        lr_host = float(lr)
+    with torch.cuda.device(param.device):
+        rc = lib.pm_step_param(param.data_ptr(), dtype_code(param), update.data_ptr(), dtype_code(update),
+                               param.numel(), lr_dev, lr_host, float(weight_decay), float(adj_ratio),
+                               stream_of(param.device))
+    check(rc, "pm_step_param")
+    del keep
+
+
+def gram(x: torch.Tensor) -> torch.Tensor:
+    """Symmetric X Xᵀ in bf16 through pm_gram (rows % 256 == 0, cols % 64 == 0)."""
+    lib = load()
+    _check_matrix(x, "x")
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("pm_gram takes a contiguous bf16 matrix")
+    rows, cols = x.shape
+    out = torch.empty((rows, rows), dtype=torch.bfloat16, device=x.device)
+    with torch.cuda.device(x.device):
+        nbytes = lib.pm_gram_workspace_bytes()
+        ws = workspace(nbytes, x.device)
+        rc = lib.pm_gram(x.data_ptr(), rows, cols, out.data_ptr(), ws.data_ptr(), nbytes, stream_of(x.device))
+    check(rc, "pm_gram")
+    return out
+
+
+def timing_enable(on: bool = True) -> None:
+    """Record a HIP event after every library launch (bench instrumentation)."""
+    load().pm_timing_enable(1 if on else 0)
+
+
+def timing_read(max_records: int = 1 << 16) -> list[dict]:
+    """Wait for the recorded launches and return one dict per launch."""
+    lib = load()
+    buf = (PmLaunchTime * max_records)()
+    n = lib.pm_timing_read(buf, max_records)
+    if n < 0:
+        check(n, "pm_timing_read")
+    return [dict(kind=KERNEL_KINDS[r.kind], group=r.group, iteration=r.iteration, n_matrices=r.n_matrices,
+                 flops=r.flops, bytes=r.bytes, ms=r.ms) for r in buf[:n]]

@@ -1,0 +1,532 @@
+// libpanmuon — C ABI (include/panmuon.h) over the gfx950 kernels of
+// pm_kernels.hpp. Host code only plans workspace, groups matrices, uploads
+// the per-call descriptor table and enqueues launches on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/panmuon.h"
+#include "pm_kernels.hpp"
+
+using namespace pm;
+
+static_assert(sizeof(BlobChunk) == 2048, "descriptor upload chunk");
+static_assert(sizeof(MatDesc) % 8 == 0, "descriptor alignment");
+// ABI layout, mirrored by the ctypes structures of pan2_amd/_lib.py
+static_assert(sizeof(pm_matrix) == 88, "pm_matrix layout");
+static_assert(sizeof(pm_ns_matrix) == 56, "pm_ns_matrix layout");
+static_assert(sizeof(pm_hparams) == 56, "pm_hparams layout");
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(PM_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+constexpr uint64_t kDefaultWorkspaceLimit = 32ull << 30;  // 32 GiB
+
+size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Shape plan of one matrix: orientation and padded extents.
+struct Plan {
+  int32_t rows, cols, trans, M, N, Mp, Np;
+  size_t ws;  // workspace bytes of this matrix
+  double flops;
+};
+
+Plan make_plan(int64_t rows, int64_t cols) {
+  Plan p{};
+  p.rows = (int32_t)rows;
+  p.cols = (int32_t)cols;
+  p.trans = rows > cols;
+  p.M = (int32_t)std::min(rows, cols);
+  p.N = (int32_t)std::max(rows, cols);
+  p.Mp = (int32_t)round_up(p.M, kTile);
+  p.Np = (int32_t)round_up(p.N, kTile);
+  const size_t x = align_up((size_t)p.Mp * p.Np * 2);
+  const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
+  const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);
+  p.ws = 4 * x + 2 * a + part + kAlign;
+  const double M = p.M, N = p.N;
+  p.flops = M * (M + 1) * N + M * M * (M + 1) + 2 * M * M * N;
+  return p;
+}
+
+// Descriptor table layout: descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1]
+size_t table_bytes(int n) {
+  return align_up((size_t)n * sizeof(MatDesc)) + 3 * align_up((size_t)(n + 1) * 4);
+}
+
+bool valid_dtype(int32_t dt) { return dt == PM_DTYPE_F32 || dt == PM_DTYPE_BF16; }
+
+int check_hparams(const pm_hparams* hp) {
+  if (!hp) return fail(PM_EINVAL, "hparams is NULL");
+  if (hp->ns_steps < 1 || hp->ns_steps >= 100)
+    return fail(PM_EUNSUPPORTED, "ns_steps must be in [1, 99], got %d", hp->ns_steps);
+  if (!(hp->eps >= 0.0f)) return fail(PM_EINVAL, "eps must be >= 0");
+  return PM_OK;
+}
+
+int check_extent(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return fail(PM_EINVAL, "matrix extents must be positive, got %lldx%lld",
+                                          (long long)rows, (long long)cols);
+  if (rows > (1 << 30) || cols > (1 << 30) || rows * cols > (1ll << 40))
+    return fail(PM_EINVAL, "matrix %lldx%lld is too large", (long long)rows, (long long)cols);
+  return PM_OK;
+}
+
+// Work item counts of one matrix.
+int32_t pro_tiles(const Plan& p) { return (p.Mp / kProTile) * (p.Np / kProTile); }
+int32_t sym_tiles(const Plan& p) {
+  const int32_t nt = p.Mp / kTile;
+  return nt * (nt + 1) / 2;
+}
+int32_t full_tiles(const Plan& p) { return (p.Mp / kTile) * (p.Np / kTile); }
+
+// One matrix of a call, whatever the entry point.
+struct Item {
+  Plan plan;
+  MatDesc desc;
+};
+
+int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
+  const uint32_t* w = (const uint32_t*)src;
+  size_t nwords = bytes / 4;
+  uint32_t* d = (uint32_t*)dst;
+  BlobChunk chunk;
+  while (nwords) {
+    const int k = (int)std::min<size_t>(nwords, 512);
+    std::memcpy(chunk.w, w, (size_t)k * 4);
+    hipLaunchKernelGGL(pm_upload_kernel, dim3(1), dim3(256), 0, stream, chunk, d, k);
+    w += k;
+    d += k;
+    nwords -= k;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "descriptor upload launch");
+}
+
+struct Coeff {
+  float a, b, c;
+};
+
+// ---- opt-in launch timing (pm_timing_enable / pm_timing_read)
+struct TimingRec {
+  pm_launch_time info;
+  hipEvent_t begin, end;
+};
+struct Timing {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  std::vector<TimingRec> recs;
+  hipEvent_t last = nullptr;
+  hipStream_t last_stream = nullptr;
+} g_timing;
+
+hipEvent_t timing_event() {
+  if (!g_timing.pool.empty()) {
+    hipEvent_t e = g_timing.pool.back();
+    g_timing.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Marks the start of a timed sequence on `stream`.
+void timing_begin(hipStream_t stream) {
+  if (!g_timing.on) return;
+  hipEvent_t e = timing_event();
+  if (!e) return;
+  hipEventRecord(e, stream);
+  g_timing.last = e;
+  g_timing.last_stream = stream;
+}
+
+// Records the end of the launch just enqueued on `stream`.
+void timing_mark(hipStream_t stream, int kind, int group, int iteration, int nmat, double flops, double bytes) {
+  if (!g_timing.on || !g_timing.last || g_timing.last_stream != stream) return;
+  hipEvent_t e = timing_event();
+  if (!e) return;
+  hipEventRecord(e, stream);
+  TimingRec r{};
+  r.info.kind = kind;
+  r.info.group = group;
+  r.info.iteration = iteration;
+  r.info.n_matrices = nmat;
+  r.info.flops = flops;
+  r.info.bytes = bytes;
+  r.begin = g_timing.last;
+  r.end = e;
+  g_timing.recs.push_back(r);
+  g_timing.last = e;
+}
+
+// Runs one group: items[lo, hi) share the workspace `ws`.
+int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
+              double lr_host, char* ws, hipStream_t stream) {
+  // Table first, then per-matrix buffers.
+  const size_t tb = table_bytes(count);
+  char* cursor = ws + tb;
+  std::vector<char> host(tb, 0);
+  MatDesc* descs = (MatDesc*)host.data();
+  int32_t* pro = (int32_t*)(host.data() + align_up((size_t)count * sizeof(MatDesc)));
+  int32_t* sym = (int32_t*)((char*)pro + align_up((size_t)(count + 1) * 4));
+  int32_t* full = (int32_t*)((char*)sym + align_up((size_t)(count + 1) * 4));
+  pro[0] = sym[0] = full[0] = 0;
+  for (int i = 0; i < count; ++i) {
+    Item& it = items[i];
+    const Plan& p = it.plan;
+    MatDesc& d = it.desc;
+    d.rows = p.rows; d.cols = p.cols; d.trans = p.trans;
+    d.M = p.M; d.N = p.N; d.Mp = p.Mp; d.Np = p.Np;
+    const size_t x = align_up((size_t)p.Mp * p.Np * 2);
+    const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
+    d.X[0] = (uint16_t*)cursor; cursor += x;
+    d.X[1] = (uint16_t*)cursor; cursor += x;
+    d.XT[0] = (uint16_t*)cursor; cursor += x;
+    d.XT[1] = (uint16_t*)cursor; cursor += x;
+    d.A = (uint16_t*)cursor; cursor += a;
+    d.B = (uint16_t*)cursor; cursor += a;
+    d.partials = (float*)cursor; cursor += align_up((size_t)pro_tiles(p) * 4);
+    d.scales = (float*)cursor; cursor += kAlign;
+    d.pro_tiles = pro_tiles(p);
+    descs[i] = d;
+    pro[i + 1] = pro[i] + pro_tiles(p);
+    sym[i + 1] = sym[i] + sym_tiles(p);
+    full[i + 1] = full[i] + full_tiles(p);
+  }
+  int rc = upload(host.data(), tb, ws, stream);
+  if (rc) return rc;
+  timing_begin(stream);
+
+  // Algorithmic work per launch (timing records only).
+  double f_gram = 0, f_poly = 0, f_upd = 0, b_pro = 0;
+  for (int i = 0; i < count; ++i) {
+    const Plan& p = items[i].plan;
+    const double M = p.M, N = p.N, elems = M * N;
+    f_gram += M * (M + 1) * N;
+    f_poly += M * M * (M + 1);
+    f_upd += 2 * M * M * N;
+    const MatDesc& d = items[i].desc;
+    const double gb = d.g_dt == PM_DTYPE_F32 ? 4 : 2;
+    const double mb = mode == MODE_STEP ? (d.m_dt == PM_DTYPE_F32 ? 8 : 4) : 0;
+    b_pro += elems * (gb + mb + 4);  // grad read, momentum read+write, X and Xᵀ bf16 writes
+  }
+
+  const MatDesc* ddesc = (const MatDesc*)ws;
+  const int32_t* dpro = (const int32_t*)(ws + ((char*)pro - host.data()));
+  const int32_t* dsym = (const int32_t*)(ws + ((char*)sym - host.data()));
+  const int32_t* dfull = (const int32_t*)(ws + ((char*)full - host.data()));
+
+  ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov};
+  hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
+  timing_mark(stream, PM_K_PROLOGUE, group, -1, count, 0.0, b_pro);
+  hipLaunchKernelGGL(pm_norm_kernel, dim3(count), dim3(kThreads), 0, stream, ddesc, hp->eps);
+  timing_mark(stream, PM_K_NORM, group, -1, count, 0.0, 0.0);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "prologue launch");
+
+  GemmArgs ga{};
+  ga.descs = ddesc;
+  ga.n = count;
+  ga.mode = mode;
+  ga.lr_dev = lr_dev;
+  ga.wd = (float)hp->weight_decay;
+  ga.wdf_host = (float)(1.0 - lr_host * (double)hp->weight_decay);
+  for (int it = 0; it < hp->ns_steps; ++it) {
+    Coeff k{hp->a, hp->b, hp->c};
+    if (hp->coeffs) k = Coeff{hp->coeffs[3 * it], hp->coeffs[3 * it + 1], hp->coeffs[3 * it + 2]};
+    ga.a = k.a; ga.b = k.b; ga.c = k.c;
+    ga.cur = it & 1;
+    ga.first = it == 0;
+    ga.prefix = dsym;
+    ga.stage = ST_GRAM;
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[count]), dim3(kThreads), 0, stream, ga);
+    timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
+    ga.stage = ST_POLY;
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_POLY>, dim3(sym[count]), dim3(kThreads), 0, stream, ga);
+    timing_mark(stream, PM_K_POLY, group, it, count, f_poly, 0.0);
+    ga.prefix = dfull;
+    const bool last = it + 1 == hp->ns_steps;
+    ga.stage = last ? ST_FINAL : ST_UPDATE;
+    if (last)
+      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_FINAL>, dim3(full[count]), dim3(kThreads), 0, stream, ga);
+    else
+      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full[count]), dim3(kThreads), 0, stream, ga);
+    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "Newton-Schulz launch");
+  }
+  return PM_OK;
+}
+
+// Sorts items by descending work (longest tiles first), packs them into
+// groups that fit the workspace and runs each group in turn.
+int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const float* lr_dev, double lr_host,
+            void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (items.empty()) return PM_OK;
+  if (!workspace) return fail(PM_EINVAL, "workspace is NULL");
+  if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
+  std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) {
+    return x.plan.Np != y.plan.Np ? x.plan.Np > y.plan.Np : x.plan.Mp > y.plan.Mp;
+  });
+  size_t i = 0;
+  int group = 0;
+  while (i < items.size()) {
+    size_t j = i, need = 0;
+    while (j < items.size()) {
+      const size_t next = need + items[j].plan.ws;
+      if (table_bytes((int)(j - i + 1)) + next > ws_bytes) break;
+      need = next;
+      ++j;
+    }
+    if (j == i)
+      return fail(PM_EWORKSPACE, "workspace of %zu bytes cannot hold a %dx%d matrix (needs %zu)", ws_bytes,
+                  items[i].plan.rows, items[i].plan.cols, table_bytes(1) + items[i].plan.ws);
+    const int rc = run_group(items.data() + i, (int)(j - i), group++, hp, mode, lr_dev, lr_host,
+                             (char*)workspace, stream);
+    if (rc) return rc;
+    i = j;
+  }
+  return PM_OK;
+}
+
+size_t plan_workspace(const std::vector<Plan>& plans, const pm_hparams* hp) {
+  size_t total = 0, largest = 0;
+  for (const Plan& p : plans) {
+    total += p.ws;
+    largest = std::max(largest, p.ws);
+  }
+  const uint64_t limit = hp->workspace_limit ? hp->workspace_limit : kDefaultWorkspaceLimit;
+  const size_t body = std::min<size_t>(total, std::max<size_t>(limit, largest));
+  return table_bytes((int)plans.size()) + body;
+}
+
+int collect_step(const pm_matrix* mats, int n, std::vector<Item>& items) {
+  if (n < 0 || (n > 0 && !mats)) return fail(PM_EINVAL, "bad matrix list");
+  items.clear();
+  items.reserve(n);
+  for (int i = 0; i < n; ++i) {
+    const pm_matrix& m = mats[i];
+    int rc = check_extent(m.rows, m.cols);
+    if (rc) return rc;
+    if (!m.param || !m.grad || !m.momentum) return fail(PM_EINVAL, "matrix %d: NULL tensor pointer", i);
+    if (!valid_dtype(m.param_dtype) || !valid_dtype(m.grad_dtype) || !valid_dtype(m.momentum_dtype))
+      return fail(PM_EDTYPE, "matrix %d: dtypes must be f32 or bf16", i);
+    if (m.param_ld < m.cols || m.grad_ld < m.cols || m.momentum_ld < m.cols)
+      return fail(PM_EINVAL, "matrix %d: row stride smaller than cols", i);
+    Item it{};
+    it.plan = make_plan(m.rows, m.cols);
+    MatDesc& d = it.desc;
+    d.param = m.param; d.grad = m.grad; d.mom = m.momentum;
+    d.p_ld = m.param_ld; d.g_ld = m.grad_ld; d.m_ld = m.momentum_ld;
+    d.p_dt = m.param_dtype; d.g_dt = m.grad_dtype; d.m_dt = m.momentum_dtype;
+    d.adj_ratio = (float)m.adj_ratio;
+    items.push_back(it);
+  }
+  return PM_OK;
+}
+
+int collect_ns(const pm_ns_matrix* mats, int n, std::vector<Item>& items) {
+  if (n < 0 || (n > 0 && !mats)) return fail(PM_EINVAL, "bad matrix list");
+  items.clear();
+  items.reserve(n);
+  for (int i = 0; i < n; ++i) {
+    const pm_ns_matrix& m = mats[i];
+    int rc = check_extent(m.rows, m.cols);
+    if (rc) return rc;
+    if (!m.in || !m.out) return fail(PM_EINVAL, "matrix %d: NULL tensor pointer", i);
+    if (!valid_dtype(m.in_dtype)) return fail(PM_EDTYPE, "matrix %d: input dtype must be f32 or bf16", i);
+    if (m.in_ld < m.cols || m.out_ld < m.cols) return fail(PM_EINVAL, "matrix %d: row stride smaller than cols", i);
+    Item it{};
+    it.plan = make_plan(m.rows, m.cols);
+    MatDesc& d = it.desc;
+    d.param = m.out; d.grad = m.in; d.mom = nullptr;
+    d.p_ld = m.out_ld; d.g_ld = m.in_ld; d.m_ld = 0;
+    d.p_dt = PM_DTYPE_BF16; d.g_dt = m.in_dtype; d.m_dt = PM_DTYPE_F32;
+    items.push_back(it);
+  }
+  return PM_OK;
+}
+
+int grid_for(int64_t n) {
+  const int64_t blocks = (n + kThreads - 1) / kThreads;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
+}
+
+}  // namespace
+
+extern "C" {
+
+int pm_abi_version(void) { return PM_ABI_VERSION; }
+
+const char* pm_last_error(void) { return g_err.c_str(); }
+
+size_t pm_workspace_bytes(const pm_matrix* mats, int n, const pm_hparams* hp) {
+  if (check_hparams(hp)) return 0;
+  std::vector<Item> items;
+  if (collect_step(mats, n, items)) return 0;
+  std::vector<Plan> plans;
+  for (auto& it : items) plans.push_back(it.plan);
+  return plan_workspace(plans, hp);
+}
+
+size_t pm_ns_workspace_bytes(const pm_ns_matrix* mats, int n, const pm_hparams* hp) {
+  if (check_hparams(hp)) return 0;
+  std::vector<Item> items;
+  if (collect_ns(mats, n, items)) return 0;
+  std::vector<Plan> plans;
+  for (auto& it : items) plans.push_back(it.plan);
+  return plan_workspace(plans, hp);
+}
+
+int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp, const float* lr_dev, double lr_host,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_hparams(hp);
+  if (rc) return rc;
+  std::vector<Item> items;
+  rc = collect_step(mats, n, items);
+  if (rc) return rc;
+  // Items are still in caller order here. The host-lr product stays in double
+  // and is rounded once, as the reference passes -adjusted_lr to its kernel.
+  for (int i = 0; i < n; ++i) items[i].desc.neg_lr_host = (float)(-(lr_host * mats[i].adj_ratio));
+  return run_all(items, hp, MODE_STEP, lr_dev, lr_host, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int pm_newton_schulz(const pm_ns_matrix* mats, int n, const pm_hparams* hp, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_hparams(hp);
+  if (rc) return rc;
+  std::vector<Item> items;
+  rc = collect_ns(mats, n, items);
+  if (rc) return rc;
+  return run_all(items, hp, MODE_NS, nullptr, 0.0, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int pm_momentum_nesterov(void* buf, int32_t buf_dtype, const void* grad, int32_t grad_dtype, void* update,
+                         int32_t update_dtype, int64_t n, float momentum, int32_t nesterov, void* stream) {
+  g_err.clear();
+  if (n < 0) return fail(PM_EINVAL, "negative element count");
+  if (n == 0) return PM_OK;
+  if (!buf || !grad || !update) return fail(PM_EINVAL, "NULL tensor pointer");
+  if (!valid_dtype(buf_dtype) || !valid_dtype(grad_dtype) || !valid_dtype(update_dtype))
+    return fail(PM_EDTYPE, "dtypes must be f32 or bf16");
+  hipLaunchKernelGGL(pm_momentum_kernel, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream, buf,
+                     buf_dtype, grad, grad_dtype, update, update_dtype, n, momentum, nesterov);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "momentum launch");
+}
+
+int pm_step_param(void* param, int32_t param_dtype, const void* update, int32_t update_dtype, int64_t n,
+                  const float* lr_dev, double lr_host, float weight_decay, double adj_ratio, void* stream) {
+  g_err.clear();
+  if (n < 0) return fail(PM_EINVAL, "negative element count");
+  if (n == 0) return PM_OK;
+  if (!param || !update) return fail(PM_EINVAL, "NULL tensor pointer");
+  if (!valid_dtype(param_dtype) || !valid_dtype(update_dtype)) return fail(PM_EDTYPE, "dtypes must be f32 or bf16");
+  const float wdf = (float)(1.0 - lr_host * (double)weight_decay);
+  const float neg = (float)(-(lr_host * adj_ratio));
+  hipLaunchKernelGGL(pm_step_kernel, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream, param,
+                     param_dtype, update, update_dtype, n, lr_dev, weight_decay, (float)adj_ratio, wdf, neg);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "step launch");
+}
+
+int pm_timing_enable(int on) {
+  g_timing.on = on != 0;
+  return PM_OK;
+}
+
+int pm_timing_read(pm_launch_time* out, int max) {
+  g_err.clear();
+  if (max < 0 || (max > 0 && !out)) return fail(PM_EINVAL, "bad output buffer");
+  int n = 0;
+  for (TimingRec& r : g_timing.recs) {
+    hipError_t e = hipEventSynchronize(r.end);
+    if (e != hipSuccess) return hip_fail(e, "timing event");
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, r.begin, r.end);
+    if (e != hipSuccess) return hip_fail(e, "timing elapsed");
+    if (n < max) {
+      out[n] = r.info;
+      out[n].ms = ms;
+      ++n;
+    }
+  }
+  // Recycle every distinct event (a record's begin is usually the previous end).
+  std::vector<hipEvent_t> used;
+  for (TimingRec& r : g_timing.recs) {
+    used.push_back(r.begin);
+    used.push_back(r.end);
+  }
+  std::sort(used.begin(), used.end());
+  used.erase(std::unique(used.begin(), used.end()), used.end());
+  g_timing.pool.insert(g_timing.pool.end(), used.begin(), used.end());
+  g_timing.recs.clear();
+  g_timing.last = nullptr;
+  return n;
+}
+
+size_t pm_gram_workspace_bytes(void) { return table_bytes(1); }
+
+int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspace, size_t workspace_bytes,
+            void* stream) {
+  g_err.clear();
+  int rc = check_extent(rows, cols);
+  if (rc) return rc;
+  if (!x || !out || !workspace) return fail(PM_EINVAL, "NULL pointer");
+  if (rows % kTile || cols % kBK) return fail(PM_EINVAL, "pm_gram needs rows %% 256 == 0 and cols %% 64 == 0");
+  if (workspace_bytes < table_bytes(1)) return fail(PM_EWORKSPACE, "workspace too small");
+  if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
+  std::vector<char> host(table_bytes(1), 0);
+  MatDesc* d = (MatDesc*)host.data();
+  d->X[0] = (uint16_t*)x;
+  d->A = (uint16_t*)out;
+  d->Mp = d->M = (int32_t)rows;
+  d->Np = d->N = (int32_t)cols;
+  d->rows = (int32_t)rows;
+  d->cols = (int32_t)cols;
+  int32_t* sym = (int32_t*)(host.data() + align_up(sizeof(MatDesc)) + align_up(8));
+  const int32_t nt = (int32_t)(rows / kTile);
+  sym[0] = 0;
+  sym[1] = nt * (nt + 1) / 2;
+  hipStream_t s = (hipStream_t)stream;
+  rc = upload(host.data(), host.size(), workspace, s);
+  if (rc) return rc;
+  GemmArgs ga{};
+  ga.descs = (const MatDesc*)workspace;
+  ga.prefix = (const int32_t*)((char*)workspace + ((char*)sym - host.data()));
+  ga.n = 1;
+  ga.stage = ST_GRAM;
+  ga.cur = 0;
+  ga.first = 0;
+  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[1]), dim3(kThreads), 0, s, ga);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "gram launch");
+}
+
+}  // extern "C"

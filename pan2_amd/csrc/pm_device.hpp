@@ -1,0 +1,125 @@
+// Device-side types and kernels of libpanmuon (gfx950 / CDNA4).
+//
+// The Muon step of one group of matrices is a fixed sequence of grouped
+// launches, each walking every matrix of the group:
+//   pm_prologue_kernel   momentum update + bf16 X/Xᵀ write + per-tile Σx²
+//   pm_norm_kernel       per-matrix 1/‖X‖ and 1/‖X‖²
+//   pm_ns_gemm_kernel    x ns_steps x {GRAM, POLY, UPDATE|FINAL}
+// The GEMM kernel is one bf16 MFMA (v_mfma_f32_32x32x16_bf16) tile engine
+// with four epilogues; every operand is K-contiguous ("NT" form), which is
+// why X is kept in both orientations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 256;       // GEMM macro tile, rows and cols
+constexpr int kBK = 64;          // K depth of one LDS stage
+constexpr int kThreads = 256;    // 4 waves of 64 lanes
+constexpr int kProTile = 64;     // prologue tile edge
+constexpr int kXcds = 8;         // MI355X: 8 XCDs, blocks dispatched round robin
+constexpr int kXcdChunk = 16;    // consecutive tiles handed to one XCD
+
+enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
+enum Stage : int32_t { ST_GRAM = 0, ST_POLY = 1, ST_UPDATE = 2, ST_FINAL = 3 };
+enum Mode : int32_t { MODE_STEP = 0, MODE_NS = 1 };
+
+// Per-matrix descriptor, resident in the workspace for the duration of a call.
+struct MatDesc {
+  // caller tensors, param layout rows x cols
+  void* param;        // MODE_STEP: parameter (in/out); MODE_NS: bf16 output
+  const void* grad;   // MODE_STEP: gradient; MODE_NS: input
+  void* mom;          // MODE_STEP: momentum buffer
+  int64_t p_ld, g_ld, m_ld;
+  int32_t rows, cols;
+  int32_t p_dt, g_dt, m_dt;
+  int32_t trans;      // rows > cols: X = uᵀ so the short side is contracted
+  int32_t M, N;       // short and long side
+  int32_t Mp, Np;     // padded to kTile (padding is zero and stays zero)
+  float adj_ratio;    // device-lr path: adjusted_lr = lr * adj_ratio
+  float neg_lr_host;  // host-lr path: -(lr * adj_ratio), rounded once
+  // workspace buffers
+  uint16_t* X[2];     // bf16 Mp x Np (ld Np), ping-pong
+  uint16_t* XT[2];    // bf16 Np x Mp (ld Mp), same values transposed
+  uint16_t* A;        // bf16 Mp x Mp gram
+  uint16_t* B;        // bf16 Mp x Mp polynomial b A + c A²
+  float* partials;    // Σx² of each prologue tile
+  float* scales;      // [0] = 1/max(‖X‖,eps)², [1] = 1/max(‖X‖,eps)
+  int32_t pro_tiles;
+  int32_t pad_;
+};
+
+struct ProArgs {
+  const MatDesc* descs;
+  const int32_t* prefix;  // n+1 prefix sums of pro_tiles
+  int32_t n;
+  int32_t mode;
+  float mu;
+  int32_t nesterov;
+};
+
+struct GemmArgs {
+  const MatDesc* descs;
+  const int32_t* prefix;  // n+1 prefix sums of this stage's tile counts
+  int32_t n;
+  int32_t stage;
+  int32_t cur;            // which X/XT ping-pong buffer holds the current X
+  int32_t first;          // iteration 0: fold the Frobenius normalisation
+  int32_t mode;
+  float a, b, c;
+  const float* lr_dev;    // device lr, or null
+  float wd;               // weight decay (device-lr path)
+  float wdf_host;         // 1 - lr*wd (host-lr path)
+};
+
+// ---------------------------------------------------------------- helpers
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  __bf16 h = (__bf16)f;  // v_cvt_pk_bf16_f32: round to nearest even, NaN kept
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float bf2f(uint16_t u) {
+  return __uint_as_float(((uint32_t)u) << 16);
+}
+__device__ __forceinline__ float load_elem(const void* p, int32_t dt, int64_t i) {
+  return dt == DT_F32 ? ((const float*)p)[i] : bf2f(((const uint16_t*)p)[i]);
+}
+__device__ __forceinline__ void store_elem(void* p, int32_t dt, int64_t i, float v) {
+  if (dt == DT_F32) ((float*)p)[i] = v;
+  else ((uint16_t*)p)[i] = f2bf(v);
+}
+
+// Locate the matrix owning global work item t: prefix[lo] <= t < prefix[lo+1].
+__device__ __forceinline__ int find_matrix(const int32_t* __restrict__ prefix, int n, int t) {
+  int lo = 0, hi = n;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (prefix[mid] <= t) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// Block b is dispatched to XCD b % 8. Hand each XCD runs of kXcdChunk
+// consecutive tiles so tiles that share operand panels share one L2.
+__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
+  constexpr int per = kXcds * kXcdChunk;
+  const int full = (nblocks / per) * per;
+  if (b >= full) return b;
+  const int w = b % per;
+  return (b - w) + (w % kXcds) * kXcdChunk + (w / kXcds);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace pm

@@ -1,0 +1,60 @@
+"""Shared test setup: the `gpu` marker and the repo root on sys.path.
+
+GPU tests call libpanmuon through its C ABI on a real MI355X; run them with
+`pytest -m gpu`. Without a HIP device they are skipped, never faked.
+"""
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an AMD MI355X (HIP device) and the built libpanmuon.so")
+
+
+def _has_gpu() -> bool:
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def pytest_collection_modifyitems(config, items):
+    if _has_gpu():
+        return
+    skip = pytest.mark.skip(reason="no HIP device in this container")
+    for item in items:
+        if "gpu" in item.keywords:
+            item.add_marker(skip)
+
+
+# torch's stock Muon functions, captured before any test installs the HIP path
+# (patch_muon replaces these module globals for the rest of the process).
+import torch.optim._muon as _torch_muon  # noqa: E402
+
+TORCH_ZEROPOWER = _torch_muon._zeropower_via_newtonschulz
+TORCH_SINGLE_TENSOR_MUON = _torch_muon._single_tensor_muon
+
+
+@pytest.fixture
+def torch_stock_muon():
+    """Run a block with torch's stock Muon functions installed, restoring after."""
+    import contextlib
+
+    @contextlib.contextmanager
+    def stock():
+        saved = (_torch_muon._zeropower_via_newtonschulz, _torch_muon._single_tensor_muon)
+        _torch_muon._zeropower_via_newtonschulz = TORCH_ZEROPOWER
+        _torch_muon._single_tensor_muon = TORCH_SINGLE_TENSOR_MUON
+        try:
+            yield
+        finally:
+            _torch_muon._zeropower_via_newtonschulz, _torch_muon._single_tensor_muon = saved
+
+    return stock
