@@ -175,8 +175,8 @@ int pm_step_param(void* param, int32_t param_dtype,
  * Symmetric gram C = X Xᵀ (bf16 in, fp32 accumulate, bf16 out) on the
  * upper-triangle tiles, mirrored. Replaces quack gemm_symmetric_out(X, X.mT)
  * (pan/optim/patch_muon.py:310). X is rows x cols with ld == cols, C is
- * rows x rows with ld == rows; rows must be a multiple of 256 and cols a
- * multiple of 64. Needs pm_gram_workspace_bytes() of workspace.
+ * rows x rows with ld == rows; rows and cols must be multiples of 256.
+ * Needs pm_gram_workspace_bytes() of workspace.
  */
 size_t pm_gram_workspace_bytes(void);
 int pm_gram(const void* x, int64_t rows, int64_t cols, void* out,

@@ -340,7 +340,7 @@ def step_param_inplace(param, update, lr, weight_decay: float, adj_ratio: float)
 
 
 def gram(x: torch.Tensor) -> torch.Tensor:
-    """Symmetric X Xᵀ in bf16 through pm_gram (rows % 256 == 0, cols % 64 == 0)."""
+    """Symmetric X Xᵀ in bf16 through pm_gram (rows and cols multiples of 256)."""
     lib = load()
     _check_matrix(x, "x")
     if x.dtype != torch.bfloat16 or not x.is_contiguous():

@@ -499,7 +499,7 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   int rc = check_extent(rows, cols);
   if (rc) return rc;
   if (!x || !out || !workspace) return fail(PM_EINVAL, "NULL pointer");
-  if (rows % kTile || cols % kBK) return fail(PM_EINVAL, "pm_gram needs rows %% 256 == 0 and cols %% 64 == 0");
+  if (rows % kTile || cols % kTile) return fail(PM_EINVAL, "pm_gram needs rows and cols that are multiples of 256");
   if (workspace_bytes < table_bytes(1)) return fail(PM_EWORKSPACE, "workspace too small");
   if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
   std::vector<char> host(table_bytes(1), 0);

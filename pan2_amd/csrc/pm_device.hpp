@@ -21,11 +21,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256;       // GEMM macro tile, rows and cols
-constexpr int kBK = 64;          // K depth of one LDS stage
+constexpr int kBK = 32;          // K depth of one LDS stage
+constexpr int kStages = 4;       // LDS stages in flight (4 x 32 KiB)
 constexpr int kThreads = 256;    // 4 waves of 64 lanes
 constexpr int kProTile = 64;     // prologue tile edge
 constexpr int kXcds = 8;         // MI355X: 8 XCDs, blocks dispatched round robin
-constexpr int kXcdChunk = 16;    // consecutive tiles handed to one XCD
+constexpr int kXcdChunk = 32;    // consecutive tiles handed to one XCD (its 32 CUs)
 
 enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
 enum Stage : int32_t { ST_GRAM = 0, ST_POLY = 1, ST_UPDATE = 2, ST_FINAL = 3 };

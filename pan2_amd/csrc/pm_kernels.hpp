@@ -2,6 +2,7 @@
 #pragma once
 
 #include "pm_device.hpp"
+#include "pm_tiles.hpp"
 
 namespace pm {
 
@@ -104,93 +105,188 @@ __global__ __launch_bounds__(kThreads) void pm_norm_kernel(const MatDesc* descs,
 //
 // C[256x256] = L[256xK] · R[256xK]ᵀ, both operands K-contiguous bf16.
 // 4 waves in a 2x2 grid, each owning 128x128 = 4x4 MFMA 32x32 tiles
-// (256 fp32 accumulators per lane, held in AGPRs). K advances 64 at a time
-// through a double-buffered LDS stage of 2 x (256x64 + 256x64) bf16 = 128 KiB.
-// LDS rows are 128 B; the 16-byte chunk index is XOR-swizzled with (row & 7)
-// so the 8 lanes of one ds_read_b128 phase hit 8 distinct chunks.
-// Global loads are buffer loads: one per-lane offset VGPR per operand, the
-// row-block and K offsets in SGPRs, and reads past the panel return zero.
+// (256 fp32 accumulators per lane, held in AGPRs).
+//
+// Operands stream through a kStages-deep ring of LDS stages, each holding
+// kBK = 32 columns of K for both operands (2 x 256 rows x 64 B = 32 KiB).
+// Global -> LDS copies are direct (buffer_load_dwordx4 ... lds): lane l of a
+// load writes 16 B at the instruction's LDS base + 16*l, so one instruction
+// fills 16 rows of 64 B and no VGPRs or ds_write instructions are spent on
+// staging. Each wave issues kLoadsPerWave such loads per stage. A stage is
+// prefetched kStages-1 stages ahead; one barrier per stage both publishes
+// the stage that landed and frees the one that was just consumed.
+//
+// LDS rows are 64 B (four 16-byte chunks). Chunk c of row r is stored at
+// chunk c ^ ((r >> 2) & 3): a ds_read_b128 phase serves 16 lanes reading 16
+// consecutive rows at one chunk, and this spreads them over 16 distinct
+// 16-byte bank groups of gfx950's 64-bank LDS.
+constexpr int kStageBytes = 2 * kTile * kBK * 2;   // 32 KiB
+constexpr int kOpBytes = kTile * kBK * 2;          // 16 KiB per operand
+constexpr int kLoadsPerWave = kOpBytes / 1024 / 4; // per operand, per stage
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint16_t* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ lds_ptr_t to_lds(char* p) {
+  return (lds_ptr_t)(__attribute__((address_space(3))) char*)p;
+}
+
+// s_waitcnt vmcnt(n), leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Block-wide barrier without the release fence of __syncthreads(), which
+// would drain every in-flight LDS DMA. Callers wait for exactly the loads they
+// need first; the "memory" clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// One LDS stage per __shared__ array, so the compiler's LDS-DMA tracking
+// sees that reads of one stage do not depend on copies into the others.
+struct Stages {
+  char* s[kStages];
+};
+
+// Fragments of one 16-deep K step: 4 A and 4 B operands of 8 bf16 each.
+struct Frags {
+  bf16x8 a[4], b[4];
+};
+
 __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, int ldl,
                                               const uint16_t* __restrict__ Rp, int ldr,
-                                              int K, char* lds, f32x16 (&acc)[4][4]) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                              int K, const Stages& st, f32x16 (&acc)[4][4]) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
   const int wm = wave >> 1, wn = wave & 1;
-  const int c = tid & 7, r0 = tid >> 3;
   const __amdgpu_buffer_rsrc_t rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
   const __amdgpu_buffer_rsrc_t rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
-  const int vl_off = r0 * ldl * 2 + c * 16;
-  const int vr_off = r0 * ldr * 2 + c * 16;
-  const int sl = 32 * ldl * 2, sr = 32 * ldr * 2;  // bytes per 32 rows
-  const int wofs = r0 * 128 + ((c ^ (r0 & 7)) << 4);
+  // Load q (0..15) of an operand covers rows 16q .. 16q+15; this wave issues
+  // q = wave*kLoadsPerWave + i. Lane l fills row 16q + l/4, stored chunk l%4,
+  // i.e. logical chunk (l%4) ^ ((l/16) & 3).
+  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const int vl_off = (lane >> 2) * ldl * 2 + lchunk * 16;
+  const int vr_off = (lane >> 2) * ldr * 2 + lchunk * 16;
+  const int q0 = wave * kLoadsPerWave;
+  // fragment reads: row rrow of a 32-row block, logical chunk 2*kk + kh
   const int rrow = lane & 31, kh = lane >> 5;
-  const int aofs = (wm * 128 + rrow) * 128;
-  const int bofs = 32768 + (wn * 128 + rrow) * 128;
+  const int rsw = (rrow >> 2) & 3;
+  const int aofs = (wm * 128 + rrow) * 64;
+  const int bofs = kOpBytes + (wn * 128 + rrow) * 64;
 
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f32x16){};
 
-  u32x4 vl[8], vr[8];
+  auto issue = [&](char* dst, int kt) {
+    const int ko = kt * kBK * 2;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    vl[j] = __builtin_amdgcn_raw_buffer_load_b128(rl, vl_off, j * sl, 0);
-    vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, vr_off, j * sr, 0);
-  }
+    for (int i = 0; i < kLoadsPerWave; ++i) {
+      const int q = q0 + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, to_lds(dst + q * 1024), 16, vl_off, q * 16 * ldl * 2 + ko, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, to_lds(dst + kOpBytes + q * 1024), 16, vr_off,
+                                               q * 16 * ldr * 2 + ko, 0, 0);
+    }
+  };
+  auto read = [&](Frags& f, const char* cur, int kk) {
+    const int sw = ((2 * kk + kh) ^ rsw) << 4;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    *(u32x4*)(lds + wofs + j * 4096) = vl[j];
-    *(u32x4*)(lds + 32768 + wofs + j * 4096) = vr[j];
-  }
-  __syncthreads();
+    for (int mi = 0; mi < 4; ++mi) f.a[mi] = *(const bf16x8*)(cur + aofs + mi * 2048 + sw);
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) f.b[ni] = *(const bf16x8*)(cur + bofs + ni * 2048 + sw);
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
+  };
 
+  // Stage kt occupies st.s[kt % 4]; it is fetched four stages ahead. Per stage:
+  //   read k-step 1 of kt      | MFMAs of k-step 0 (read one stage earlier)
+  //   stage kt+1 landed? barrier; refill kt's buffer with kt+4; read k-step 0 of kt+1
+  //   MFMAs of k-step 1
+  // so no MFMA waits on an LDS read issued just before it.
+  // `pending` = stages issued after kt+1 that may stay in flight at the barrier.
+  // Instruction order within a stage is pinned: sched_barrier(0) closes each
+  // region and sched_group_barrier lays the region out as single MFMAs with
+  // one memory instruction between them, so every LDS read and DMA issue
+  // hides under an MFMA already in flight. Only the barrier stalls the MFMAs.
+  //   region 1: 16 MFMAs of k-step 0 of kt, interleaved with the 8 reads of k-step 1
+  //   wait: k-step 1 read, stage kt+1 landed; barrier
+  //   region 2: 16 MFMAs of k-step 1, interleaved with the 8 reads of k-step 0
+  //             of kt+1, then the 8 DMA loads of stage kt+4 (into kt's buffer)
+  constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
+  Frags f0, f1;
+  auto body = [&](int s, int kt, bool has_next, int pending, bool refill) {
+    read(f1, st.s[s], 1);
+    mma(f0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
+      if (pending == 2) wait_vmcnt<2 * 2 * kLoadsPerWave>();
+      else if (pending == 1) wait_vmcnt<1 * 2 * kLoadsPerWave>();
+      else wait_vmcnt<0>();
+      block_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (refill) issue(st.s[s], kt + kStages);
+      read(f0, st.s[(s + 1) % kStages], 0);
+    }
+    mma(f1);
+    if (has_next) {
+      // reads of the next k-step first, so they land long before region 1 uses them
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+        if (refill) __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 1);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Every caller passes K a multiple of kTile (padded extents), so KT = K / kBK
+  // is a multiple of kStages and at least 2 * kStages.
+  static_assert(kStages == 4, "one __shared__ array per stage; waits below assume four");
   const int KT = K / kBK;
-  for (int kt = 0; kt < KT; ++kt) {
-    char* cur = lds + (kt & 1) * 65536;
-    char* nxt = lds + ((kt + 1) & 1) * 65536;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      const int ko = (kt + 1) * kBK * 2;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        vl[j] = __builtin_amdgcn_raw_buffer_load_b128(rl, vl_off, j * sl + ko, 0);
-        vr[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, vr_off, j * sr + ko, 0);
-      }
-    }
+  for (int s = 0; s < kStages; ++s) issue(st.s[s], s);
+  wait_vmcnt<3 * 2 * kLoadsPerWave>();
+  block_barrier();
+  read(f0, st.s[0], 0);
+
+  for (int kt0 = 0; kt0 < KT - kStages; kt0 += kStages) {
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int sw = ((2 * kk + kh) ^ (rrow & 7)) << 4;
-      bf16x8 a[4], b[4];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi) a[mi] = *(const bf16x8*)(cur + aofs + mi * 4096 + sw);
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) b[ni] = *(const bf16x8*)(cur + bofs + ni * 4096 + sw);
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
-    }
-    if (more) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        *(u32x4*)(nxt + wofs + j * 4096) = vl[j];
-        *(u32x4*)(nxt + 32768 + wofs + j * 4096) = vr[j];
-      }
-    }
-    __syncthreads();
+    for (int s = 0; s < kStages; ++s) body(s, kt0 + s, true, 2, true);
   }
+  const int kt0 = KT - kStages;
+  body(0, kt0, true, 2, false);
+  body(1, kt0 + 1, true, 1, false);
+  body(2, kt0 + 2, true, 0, false);
+  body(3, kt0 + 3, false, 0, false);
 }
 
-// Visits this lane's accumulators as quads: f(p0, q, x) gets rows p0..p0+3 of
-// column q. (v_mfma 32x32 layout: lane l, register r -> row 8*(r/4) +
-// 4*(l/32) + r%4, column l%32.) Indices are compile-time after unrolling, so
-// the accumulators stay in registers.
+// Visits this lane's accumulators as quads: f(i, p0, q, x) gets rows
+// p0..p0+3 of column q, i = 0..63 the quad's index. (v_mfma 32x32 layout:
+// lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.) Indices
+// are compile-time after unrolling, so the accumulators stay in registers.
 template <class F>
 __device__ __forceinline__ void for_each_quad(const f32x16 (&acc)[4][4], int pbase, int qbase, F&& f) {
 #pragma unroll
@@ -201,8 +297,22 @@ __device__ __forceinline__ void for_each_quad(const f32x16 (&acc)[4][4], int pba
       for (int g = 0; g < 4; ++g) {
         const float x[4] = {acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2],
                             acc[mi][ni][4 * g + 3]};
-        f(pbase + mi * 32 + 8 * g, qbase + ni * 32, x);
+        f((mi * 4 + ni) * 4 + g, pbase + mi * 32 + 8 * g, qbase + ni * 32, x);
       }
+}
+
+// Loads, for every quad of this lane, the 4 consecutive elements T[q][p0..p0+3]
+// of a row-major matrix T (ld elements): 8-byte loads, all issued before use.
+__device__ __forceinline__ void load_quads(u16x4 (&v)[64], const uint16_t* __restrict__ T, int64_t ld,
+                                           int pbase, int qbase) {
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        v[(mi * 4 + ni) * 4 + g] =
+            *(const u16x4*)(T + (int64_t)(qbase + ni * 32) * ld + pbase + mi * 32 + 8 * g);
 }
 
 // Operands and tile of one work item of stage STAGE.
@@ -230,15 +340,10 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
     j.L = d.XT[cur]; j.ldl = d.Mp; j.R = d.B; j.ldr = d.Mp; j.K = d.Mp; P = d.Np; Q = d.Mp;
   }
   if (sym) {
-    const int nt = P / kTile;
-    int rem = lt, i = 0;
-    while (rem >= nt - i) { rem -= nt - i; ++i; }
-    j.ti = i; j.tj = i + rem;
+    sym_tile(lt, P / kTile, j.ti, j.tj);
   } else {
-    const int ntq = Q / kTile;
-    j.ti = lt / ntq; j.tj = lt - j.ti * ntq;
+    full_tile(lt, P / kTile, Q / kTile, j.ti, j.tj);
   }
-  (void)P;
   return j;
 }
 
@@ -256,7 +361,12 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
 template <int STAGE>
 __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) char lds[4 * 32768];
+  __shared__ __attribute__((aligned(1024))) char lds0[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char lds1[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char lds2[kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char lds3[kStageBytes];
+  static_assert(kStages == 4, "one __shared__ array per stage");
+  const Stages st{{lds0, lds1, lds2, lds3}};
 
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int m = find_matrix(args.prefix, args.n, t);
@@ -266,27 +376,31 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
 
   f32x16 acc[4][4];
   gemm_mainloop(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl, job.R + (int64_t)job.tj * kTile * job.ldr,
-                job.ldr, job.K, lds, acc);
+                job.ldr, job.K, st, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pbase = job.ti * kTile + (wave >> 1) * 128 + 4 * (lane >> 5);
   const int qbase = job.tj * kTile + (wave & 1) * 128 + (lane & 31);
 
+  // Epilogue operands are read as quads T[q][p0..p0+3] from the orientation
+  // whose rows run along this lane's 4 consecutive output rows p: A is
+  // symmetric, and X / Xᵀ hold the same values transposed. All loads are
+  // issued before any store, so no load waits behind stores in vmcnt order.
   if (STAGE == ST_GRAM || STAGE == ST_POLY) {
     uint16_t* C = (STAGE == ST_GRAM) ? d.A : d.B;
-    const uint16_t* A = d.A;
     const int64_t ldc = d.Mp;
     const float s = (STAGE == ST_GRAM && args.first) ? d.scales[0] : 1.0f;
     const float cb = args.b, cc = args.c;
     const bool mirror = job.ti != job.tj;
-    for_each_quad(acc, pbase, qbase, [&](int p0, int q, const float (&x)[4]) {
+    u16x4 av[64];
+    if (STAGE == ST_POLY) load_quads(av, d.A, ldc, pbase, qbase);
+    for_each_quad(acc, pbase, qbase, [&](int i, int p0, int q, const float (&x)[4]) {
       u16x4 o;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t off = (int64_t)(p0 + r) * ldc + q;
-        const float v = (STAGE == ST_GRAM) ? x[r] * s : cc * x[r] + cb * bf2f(A[off]);
+        const float v = (STAGE == ST_GRAM) ? x[r] * s : cc * x[r] + cb * bf2f(av[i][r]);
         o[r] = f2bf(v);
-        C[off] = o[r];
+        C[(int64_t)(p0 + r) * ldc + q] = o[r];
       }
       if (mirror) *(u16x4*)(C + (int64_t)q * ldc + p0) = o;
     });
@@ -296,76 +410,80 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
   const float s = args.first ? d.scales[1] : 1.0f;
   const float ca = args.a;
   if (STAGE == ST_UPDATE) {
-    const uint16_t* Xc = d.X[cur];
     uint16_t* Xn = d.X[cur ^ 1];
     uint16_t* XTn = d.XT[cur ^ 1];
     const int64_t ldx = d.Np, ldxt = d.Mp;
-    for_each_quad(acc, pbase, qbase, [&](int p0, int q, const float (&x)[4]) {
+    u16x4 xv[64];
+    load_quads(xv, d.XT[cur], ldxt, pbase, qbase);  // X[p][q] = Xᵀ[q][p]
+    for_each_quad(acc, pbase, qbase, [&](int i, int p0, int q, const float (&x)[4]) {
       u16x4 o;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t off = (int64_t)(p0 + r) * ldx + q;
-        o[r] = f2bf((ca * bf2f(Xc[off]) + x[r]) * s);
-        Xn[off] = o[r];
+        o[r] = f2bf((ca * bf2f(xv[i][r]) + x[r]) * s);
+        Xn[(int64_t)(p0 + r) * ldx + q] = o[r];
       }
       *(u16x4*)(XTn + (int64_t)q * ldxt + p0) = o;
     });
     return;
   }
 
-  // ST_FINAL: P rows / Q cols are the param's own rows / cols.
-  const uint16_t* Xt = d.trans ? d.XT[cur] : d.X[cur];
-  const int64_t ldx = d.trans ? d.Mp : d.Np;
+  // ST_FINAL: P rows / Q cols are the param's own rows / cols; the a·X term
+  // is X[p][q] (wide) or Xᵀ[p][q] (tall), read from the other orientation.
+  // Work goes one 32-row band (16 quads) at a time to bound register use; a
+  // band's loads are all issued before its stores.
+  const uint16_t* T = d.trans ? d.X[cur] : d.XT[cur];
+  const int64_t ldt = d.trans ? d.Np : d.Mp;
   const int rows = d.rows, cols = d.cols;
   const int64_t ldp = d.p_ld;
-  if (args.mode == MODE_NS) {
-    uint16_t* out = (uint16_t*)d.param;
-    for_each_quad(acc, pbase, qbase, [&](int p0, int q, const float (&x)[4]) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int p = p0 + r;
-        const float v = (ca * bf2f(Xt[(int64_t)p * ldx + q]) + x[r]) * s;
-        if (p < rows && q < cols) out[(int64_t)p * ldp + q] = f2bf(v);
-      }
-    });
-    return;
+  float wdf = 0.0f, neg = 0.0f;
+  if (args.mode == MODE_STEP) {
+    if (args.lr_dev) {
+      const float lr = *args.lr_dev;
+      wdf = 1.0f - lr * args.wd;
+      neg = -(lr * d.adj_ratio);
+    } else {
+      wdf = args.wdf_host;
+      neg = d.neg_lr_host;
+    }
   }
-  float wdf, neg;
-  if (args.lr_dev) {
-    const float lr = *args.lr_dev;
-    wdf = 1.0f - lr * args.wd;
-    neg = -(lr * d.adj_ratio);
-  } else {
-    wdf = args.wdf_host;
-    neg = d.neg_lr_host;
-  }
-  if (d.p_dt == DT_F32) {
-    float* P = (float*)d.param;
-    for_each_quad(acc, pbase, qbase, [&](int p0, int q, const float (&x)[4]) {
+  auto final_bands = [&](auto* P, auto load, auto store, bool step) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int p = p0 + r;
-        const float o = bf2f(f2bf((ca * bf2f(Xt[(int64_t)p * ldx + q]) + x[r]) * s));
-        if (p < rows && q < cols) {
-          const int64_t po = (int64_t)p * ldp + q;
-          P[po] = P[po] * wdf + o * neg;
+    for (int mi = 0; mi < 4; ++mi) {
+      u16x4 xv[16];
+      float pv[16][4];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int ni = j >> 2, g = j & 3;
+        const int p0 = pbase + mi * 32 + 8 * g, q = qbase + ni * 32;
+        xv[j] = *(const u16x4*)(T + (int64_t)q * ldt + p0);
+        if (step) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int p = p0 + r;
+            pv[j][r] = (p < rows && q < cols) ? load(P + (int64_t)p * ldp + q) : 0.0f;
+          }
         }
       }
-    });
-  } else {
-    uint16_t* P = (uint16_t*)d.param;
-    for_each_quad(acc, pbase, qbase, [&](int p0, int q, const float (&x)[4]) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int p = p0 + r;
-        const float o = bf2f(f2bf((ca * bf2f(Xt[(int64_t)p * ldx + q]) + x[r]) * s));
-        if (p < rows && q < cols) {
-          const int64_t po = (int64_t)p * ldp + q;
-          P[po] = f2bf(bf2f(P[po]) * wdf + o * neg);
+      for (int j = 0; j < 16; ++j) {
+        const int ni = j >> 2, g = j & 3;
+        const int p0 = pbase + mi * 32 + 8 * g, q = qbase + ni * 32;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = p0 + r;
+          const float o = bf2f(f2bf((ca * bf2f(xv[j][r]) + acc[mi][ni][4 * g + r]) * s));
+          if (p < rows && q < cols) store(P + (int64_t)p * ldp + q, step ? pv[j][r] * wdf + o * neg : o);
         }
       }
-    });
-  }
+    }
+  };
+  auto ld_f32 = [](const float* a) { return *a; };
+  auto st_f32 = [](float* a, float v) { *a = v; };
+  auto ld_bf16 = [](const uint16_t* a) { return bf2f(*a); };
+  auto st_bf16 = [](uint16_t* a, float v) { *a = f2bf(v); };
+  if (args.mode == MODE_NS) final_bands((uint16_t*)d.param, ld_bf16, st_bf16, false);
+  else if (d.p_dt == DT_F32) final_bands((float*)d.param, ld_f32, st_f32, true);
+  else final_bands((uint16_t*)d.param, ld_bf16, st_bf16, true);
 }
 
 // ============================================================ elementwise

@@ -1,0 +1,54 @@
+// Work-item -> tile decoders of the GEMM stages. Plain arithmetic, compiled
+// for the device by hipcc and for the host by the CPU tests (g++).
+#pragma once
+
+#if defined(__HIPCC__)
+#define PM_HD __host__ __device__ __forceinline__
+#else
+#define PM_HD inline
+#endif
+
+namespace pm {
+
+// Consecutive work items walk kGroupRows tile rows column by column, so the
+// 32 tiles an XCD runs together form a kGroupRows x 8 block that shares
+// kGroupRows row panels and 8 column panels in that XCD's L2.
+constexpr int kGroupRows = 4;
+
+PM_HD int imin(int a, int b) { return a < b ? a : b; }
+
+// Rectangular np x nq tile grid; lt in [0, np*nq).
+PM_HD void full_tile(int lt, int np, int nq, int& ti, int& tj) {
+  const int per_group = kGroupRows * nq;
+  const int g = lt / per_group;
+  const int g0 = g * kGroupRows;
+  const int gm = imin(kGroupRows, np - g0);
+  const int r = lt - g * per_group;
+  ti = g0 + r % gm;
+  tj = r / gm;
+}
+
+// Upper triangle (ti <= tj) of an nt x nt tile grid, grouped the same way;
+// lt in [0, nt*(nt+1)/2).
+PM_HD void sym_tile(int lt, int nt, int& ti, int& tj) {
+  int rem = lt, g0 = 0, gm = 0;
+  for (;; g0 += kGroupRows) {
+    gm = imin(kGroupRows, nt - g0);
+    const int cnt = gm * (gm + 1) / 2 + (nt - g0 - gm) * gm;
+    if (rem < cnt) break;
+    rem -= cnt;
+  }
+  const int tri = gm * (gm + 1) / 2;
+  if (rem < tri) {  // columns g0 .. g0+gm-1 hold 1 .. gm tiles of the group
+    int c = 0;
+    while ((c + 1) * (c + 2) / 2 <= rem) ++c;
+    ti = g0 + (rem - c * (c + 1) / 2);
+    tj = g0 + c;
+  } else {
+    rem -= tri;
+    ti = g0 + rem % gm;
+    tj = g0 + gm + rem / gm;
+  }
+}
+
+}  // namespace pm

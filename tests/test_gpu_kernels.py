@@ -29,7 +29,7 @@ def rel_fro(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
 
-@pytest.mark.parametrize("rows,cols", [(256, 64), (512, 1024), (1024, 4096), (768, 320)])
+@pytest.mark.parametrize("rows,cols", [(256, 256), (512, 1024), (1024, 4096), (768, 512)])
 def test_gram_symmetric_vs_fp64(rows, cols):
     print(f"gram {rows}x{cols}", flush=True)
     x = seeded((rows, cols), 11 + rows).to(torch.bfloat16)
@@ -42,6 +42,12 @@ def test_gram_symmetric_vs_fp64(rows, cols):
     err = np.abs(c - ref)
     assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-3 * np.abs(ref).max()), float(err.max())
     assert np.array_equal(c, round_bf16(c)), "output must be bf16 values"
+
+
+def test_gram_rejects_unpadded_shapes():
+    x = torch.zeros((256, 320), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="multiples of 256"):
+        _lib.gram(x)
 
 
 NS_SHAPES = [(256, 256), (1024, 4096), (4096, 1024), (300, 700), (700, 300), (64, 96), (513, 257)]
