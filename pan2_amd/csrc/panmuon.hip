@@ -263,18 +263,18 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     ga.first = it == 0;
     ga.prefix = dsym;
     ga.stage = ST_GRAM;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[count]), dim3(kThreads), 0, stream, ga);
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[count]), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
     ga.stage = ST_POLY;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_POLY>, dim3(sym[count]), dim3(kThreads), 0, stream, ga);
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_POLY>, dim3(sym[count]), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, PM_K_POLY, group, it, count, f_poly, 0.0);
     ga.prefix = dfull;
     const bool last = it + 1 == hp->ns_steps;
     ga.stage = last ? ST_FINAL : ST_UPDATE;
     if (last)
-      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_FINAL>, dim3(full[count]), dim3(kThreads), 0, stream, ga);
+      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_FINAL>, dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
     else
-      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full[count]), dim3(kThreads), 0, stream, ga);
+      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "Newton-Schulz launch");
@@ -524,7 +524,7 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   ga.stage = ST_GRAM;
   ga.cur = 0;
   ga.first = 0;
-  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[1]), dim3(kThreads), 0, s, ga);
+  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[1]), dim3(kGemmThreads), 0, s, ga);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PM_OK : hip_fail(e, "gram launch");
 }

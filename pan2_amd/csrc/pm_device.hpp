@@ -23,7 +23,8 @@ typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 constexpr int kTile = 256;       // GEMM macro tile, rows and cols
 constexpr int kBK = 32;          // K depth of one LDS stage
 constexpr int kStages = 4;       // LDS stages in flight (4 x 32 KiB)
-constexpr int kThreads = 256;    // 4 waves of 64 lanes
+constexpr int kThreads = 256;    // elementwise/prologue blocks: 4 waves of 64 lanes
+constexpr int kGemmThreads = 512;  // GEMM blocks: 8 waves, two per SIMD
 constexpr int kProTile = 64;     // prologue tile edge
 constexpr int kXcds = 8;         // MI355X: 8 XCDs, blocks dispatched round robin
 constexpr int kXcdChunk = 32;    // consecutive tiles handed to one XCD (its 32 CUs)

@@ -104,25 +104,29 @@ __global__ __launch_bounds__(kThreads) void pm_norm_kernel(const MatDesc* descs,
 // ============================================================ GEMM engine
 //
 // C[256x256] = L[256xK] · R[256xK]ᵀ, both operands K-contiguous bf16.
-// 4 waves in a 2x2 grid, each owning 128x128 = 4x4 MFMA 32x32 tiles
-// (256 fp32 accumulators per lane, held in AGPRs).
+// 8 waves, two per SIMD, in a 2 (rows) x 4 (cols) grid; each owns a 128x64
+// sub-tile = 4x2 MFMA 32x32 tiles (128 fp32 accumulators per lane in AGPRs),
+// so the two waves of a SIMD take turns issuing MFMAs while the other one
+// waits on memory or the barrier.
 //
 // Operands stream through a kStages-deep ring of LDS stages, each holding
 // kBK = 32 columns of K for both operands (2 x 256 rows x 64 B = 32 KiB).
 // Global -> LDS copies are direct (buffer_load_dwordx4 ... lds): lane l of a
 // load writes 16 B at the instruction's LDS base + 16*l, so one instruction
 // fills 16 rows of 64 B and no VGPRs or ds_write instructions are spent on
-// staging. Each wave issues kLoadsPerWave such loads per stage. A stage is
-// prefetched kStages-1 stages ahead; one barrier per stage both publishes
-// the stage that landed and frees the one that was just consumed.
+// staging. Each wave issues kLoadsPerWave such loads per operand per stage.
 //
 // LDS rows are 64 B (four 16-byte chunks). Chunk c of row r is stored at
 // chunk c ^ ((r >> 2) & 3): a ds_read_b128 phase serves 16 lanes reading 16
 // consecutive rows at one chunk, and this spreads them over 16 distinct
-// 16-byte bank groups of gfx950's 64-bank LDS.
+// 16-byte bank groups of gfx950's 64-bank LDS (measured conflict-free).
 constexpr int kStageBytes = 2 * kTile * kBK * 2;   // 32 KiB
 constexpr int kOpBytes = kTile * kBK * 2;          // 16 KiB per operand
-constexpr int kLoadsPerWave = kOpBytes / 1024 / 4; // per operand, per stage
+constexpr int kWaves = kGemmThreads / 64;          // 8
+constexpr int kLoadsPerWave = kOpBytes / 1024 / kWaves;  // per operand, per stage
+constexpr int kWaveRows = 128, kWaveCols = 64;     // per-wave sub-tile
+constexpr int kMi = kWaveRows / 32, kNi = kWaveCols / 32;
+constexpr int kQuads = kMi * kNi * 4;              // accumulator quads per lane
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint16_t* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
@@ -153,17 +157,36 @@ struct Stages {
   char* s[kStages];
 };
 
-// Fragments of one 16-deep K step: 4 A and 4 B operands of 8 bf16 each.
+// Fragments of one LDS stage (two 16-deep K steps) of this wave's sub-tile.
 struct Frags {
-  bf16x8 a[4], b[4];
+  bf16x8 a[2][kMi], b[2][kNi];
 };
 
+// Ping-pong schedule. Waves 0-3 (group A, rows 0-127) and 4-7 (group B, rows
+// 128-255) put one wave of each group on every SIMD. Every wave runs the same
+// program, a sequence of slots closed by block barriers:
+//   M(-1) | C(0) | M(0) | C(1) | M(1) | ...
+//   C(k): the 16 MFMAs of stage k, with this wave's share of the DMA loads of
+//         stage k+3 (into buffer (k-1)%4) issued one per 4 MFMAs
+//   M(k): the LDS reads of this wave's fragments of stage k+1
+// but group B enters one slot later (one extra barrier up front, A adds one at
+// the end), so on every SIMD one wave streams MFMAs while the other reads LDS.
+// Issuing the DMA from the compute slot spreads it evenly over time: the
+// CU's vector-memory address path (about 55 B/clk measured) stays well below
+// saturation and an issue rarely blocks, whereas a burst of DMA issues at the
+// start of a memory slot made that slot, and the barrier, wait for it.
+// Ordering: stage k is read by A in slot 2k-1 and by B in slot 2k (closed by
+// lgkmcnt(0)); A's C(k+1) (slot 2k+2) and B's C(k+1) (slot 2k+3) refill its
+// buffer, after both. Each slot ends with this wave's share of the next stage
+// anyone reads waited for (k+1 after C(k), k+2 after M(k)). Stage k lives in
+// __shared__ array k % 4.
 __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, int ldl,
                                               const uint16_t* __restrict__ Rp, int ldr,
-                                              int K, const Stages& st, f32x16 (&acc)[4][4]) {
+                                              int K, const Stages& st, f32x16 (&acc)[kMi][kNi]) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wr = wave >> 2, wc = wave & 3;
+  const bool group_b = wr != 0;
   const __amdgpu_buffer_rsrc_t rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
   const __amdgpu_buffer_rsrc_t rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
   // Load q (0..15) of an operand covers rows 16q .. 16q+15; this wave issues
@@ -176,14 +199,15 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
   // fragment reads: row rrow of a 32-row block, logical chunk 2*kk + kh
   const int rrow = lane & 31, kh = lane >> 5;
   const int rsw = (rrow >> 2) & 3;
-  const int aofs = (wm * 128 + rrow) * 64;
-  const int bofs = kOpBytes + (wn * 128 + rrow) * 64;
+  const int aofs = (wr * kWaveRows + rrow) * 64;
+  const int bofs = kOpBytes + (wc * kWaveCols + rrow) * 64;
 
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f32x16){};
+    for (int ni = 0; ni < kNi; ++ni) acc[mi][ni] = (f32x16){};
 
+  constexpr int kDma = 2 * kLoadsPerWave;  // this wave's loads per stage
   auto issue = [&](char* dst, int kt) {
     const int ko = kt * kBK * 2;
 #pragma unroll
@@ -194,124 +218,127 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
                                                q * 16 * ldr * 2 + ko, 0, 0);
     }
   };
-  auto read = [&](Frags& f, const char* cur, int kk) {
-    const int sw = ((2 * kk + kh) ^ rsw) << 4;
+  auto read = [&](Frags& f, const char* cur) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) f.a[mi] = *(const bf16x8*)(cur + aofs + mi * 2048 + sw);
+    for (int kk = 0; kk < 2; ++kk) {
+      const int sw = ((2 * kk + kh) ^ rsw) << 4;
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) f.b[ni] = *(const bf16x8*)(cur + bofs + ni * 2048 + sw);
-  };
-  auto mma = [&](const Frags& f) {
+      for (int mi = 0; mi < kMi; ++mi) f.a[kk][mi] = *(const bf16x8*)(cur + aofs + mi * 2048 + sw);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mi], f.b[ni], acc[mi][ni], 0, 0, 0);
-  };
-
-  // Stage kt occupies st.s[kt % 4]; it is fetched four stages ahead. Per stage:
-  //   read k-step 1 of kt      | MFMAs of k-step 0 (read one stage earlier)
-  //   stage kt+1 landed? barrier; refill kt's buffer with kt+4; read k-step 0 of kt+1
-  //   MFMAs of k-step 1
-  // so no MFMA waits on an LDS read issued just before it.
-  // `pending` = stages issued after kt+1 that may stay in flight at the barrier.
-  // Instruction order within a stage is pinned: sched_barrier(0) closes each
-  // region and sched_group_barrier lays the region out as single MFMAs with
-  // one memory instruction between them, so every LDS read and DMA issue
-  // hides under an MFMA already in flight. Only the barrier stalls the MFMAs.
-  //   region 1: 16 MFMAs of k-step 0 of kt, interleaved with the 8 reads of k-step 1
-  //   wait: k-step 1 read, stage kt+1 landed; barrier
-  //   region 2: 16 MFMAs of k-step 1, interleaved with the 8 reads of k-step 0
-  //             of kt+1, then the 8 DMA loads of stage kt+4 (into kt's buffer)
-  constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
-  Frags f0, f1;
-  auto body = [&](int s, int kt, bool has_next, int pending, bool refill) {
-    read(f1, st.s[s], 1);
-    mma(f0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+      for (int ni = 0; ni < kNi; ++ni) f.b[kk][ni] = *(const bf16x8*)(cur + bofs + ni * 2048 + sw);
     }
-    __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+  };
+  constexpr int kMfma = 0x008, kVmemRead = 0x020;
+  constexpr int kMfmas = 2 * kMi * kNi;
+  static_assert(kMfmas % kDma == 0, "DMA issues must split the MFMAs evenly");
+  // C slot: the stage's MFMAs, with `dst`'s DMA (stage kt) spread among them
+  auto compute = [&](const Frags& f, char* dst, int kt, bool refill) {
+    __builtin_amdgcn_s_setprio(1);
+    if (refill) issue(dst, kt);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < kNi; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[kk][mi], f.b[kk][ni], acc[mi][ni], 0, 0, 0);
+    if (refill) {
+#pragma unroll
+      for (int i = 0; i < kDma; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, kMfmas / kDma, 0);
+        __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if (has_next) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
-      if (pending == 2) wait_vmcnt<2 * 2 * kLoadsPerWave>();
-      else if (pending == 1) wait_vmcnt<1 * 2 * kLoadsPerWave>();
-      else wait_vmcnt<0>();
-      block_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      if (refill) issue(st.s[s], kt + kStages);
-      read(f0, st.s[(s + 1) % kStages], 0);
-    }
-    mma(f1);
-    if (has_next) {
-      // reads of the next k-step first, so they land long before region 1 uses them
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 1);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
-        if (refill) __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 1);
-      }
-    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // this wave's DMA of a stage landed, with `pending` later stages in flight
+  auto wait_loads = [&](int pending) {
+    if (pending >= 2) wait_vmcnt<2 * kDma>();
+    else if (pending == 1) wait_vmcnt<kDma>();
+    else wait_vmcnt<0>();
+  };
+  auto slot_end = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    block_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
 
   // Every caller passes K a multiple of kTile (padded extents), so KT = K / kBK
   // is a multiple of kStages and at least 2 * kStages.
-  static_assert(kStages == 4, "one __shared__ array per stage; waits below assume four");
+  static_assert(kStages == 4, "one __shared__ array per stage; schedule assumes four");
   const int KT = K / kBK;
-#pragma unroll
-  for (int s = 0; s < kStages; ++s) issue(st.s[s], s);
-  wait_vmcnt<3 * 2 * kLoadsPerWave>();
-  block_barrier();
-  read(f0, st.s[0], 0);
+  Frags f;
 
-  for (int kt0 = 0; kt0 < KT - kStages; kt0 += kStages) {
 #pragma unroll
-    for (int s = 0; s < kStages; ++s) body(s, kt0 + s, true, 2, true);
+  for (int s = 0; s < kStages - 1; ++s) issue(st.s[s], s);
+  wait_loads(2);  // stage 0 (stages 1, 2 may stay in flight)
+  slot_end();
+  if (group_b) slot_end();  // B enters one slot later
+  // M(-1): fragments of stage 0; stage 1 landed (this wave's share)
+  read(f, st.s[0]);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  wait_loads(1);
+  slot_end();
+
+  // Stage k in buffer s = k % 4. `refill`: stage k+3 exists (DMA'd during
+  // C(k)); `pend1` / `pend2`: stages allowed in flight after stage k+1 at the
+  // end of C(k) / after stage k+2 at the end of M(k); `next` / `next2`: stage
+  // k+1 / k+2 exists.
+  auto stage = [&](int s, int k, bool refill, int pend1, int pend2, bool next, bool next2) {
+    compute(f, st.s[(s + kStages - 1) % kStages], k + kStages - 1, refill);
+    if (next) wait_loads(pend1);
+    slot_end();
+    if (next) {
+      read(f, st.s[(s + 1) % kStages]);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): buffer (k+1)%4 read before it is refilled
+    }
+    if (next2) wait_loads(pend2);
+    slot_end();
+  };
+
+  for (int k0 = 0; k0 < KT - kStages; k0 += kStages) {
+#pragma unroll
+    for (int s = 0; s < kStages; ++s) stage(s, k0 + s, true, 2, 1, true, true);
   }
-  const int kt0 = KT - kStages;
-  body(0, kt0, true, 2, false);
-  body(1, kt0 + 1, true, 1, false);
-  body(2, kt0 + 2, true, 0, false);
-  body(3, kt0 + 3, false, 0, false);
+  const int k0 = KT - kStages;
+  // tail: stages issued by the end of C(k) / M(k) run to min(KT-1, k+3)
+  stage(0, k0, true, 2, 1, true, true);      // issues KT-1
+  stage(1, k0 + 1, false, 1, 0, true, true);
+  stage(2, k0 + 2, false, 0, 0, true, false);
+  stage(3, k0 + 3, false, 0, 0, false, false);
+  if (!group_b) slot_end();  // match B's extra barrier
 }
 
 // Visits this lane's accumulators as quads: f(i, p0, q, x) gets rows
-// p0..p0+3 of column q, i = 0..63 the quad's index. (v_mfma 32x32 layout:
-// lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.) Indices
-// are compile-time after unrolling, so the accumulators stay in registers.
+// p0..p0+3 of column q, i the quad's index. (v_mfma 32x32 layout: lane l,
+// register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.) Indices are
+// compile-time after unrolling, so the accumulators stay in registers.
 template <class F>
-__device__ __forceinline__ void for_each_quad(const f32x16 (&acc)[4][4], int pbase, int qbase, F&& f) {
+__device__ __forceinline__ void for_each_quad(const f32x16 (&acc)[kMi][kNi], int pbase, int qbase, F&& f) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
+    for (int ni = 0; ni < kNi; ++ni)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float x[4] = {acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2],
                             acc[mi][ni][4 * g + 3]};
-        f((mi * 4 + ni) * 4 + g, pbase + mi * 32 + 8 * g, qbase + ni * 32, x);
+        f((mi * kNi + ni) * 4 + g, pbase + mi * 32 + 8 * g, qbase + ni * 32, x);
       }
 }
 
 // Loads, for every quad of this lane, the 4 consecutive elements T[q][p0..p0+3]
 // of a row-major matrix T (ld elements): 8-byte loads, all issued before use.
-__device__ __forceinline__ void load_quads(u16x4 (&v)[64], const uint16_t* __restrict__ T, int64_t ld,
+__device__ __forceinline__ void load_quads(u16x4 (&v)[kQuads], const uint16_t* __restrict__ T, int64_t ld,
                                            int pbase, int qbase) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
+    for (int ni = 0; ni < kNi; ++ni)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        v[(mi * 4 + ni) * 4 + g] =
+        v[(mi * kNi + ni) * 4 + g] =
             *(const u16x4*)(T + (int64_t)(qbase + ni * 32) * ld + pbase + mi * 32 + 8 * g);
 }
 
@@ -359,7 +386,7 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
 // each off-diagonal tile is also stored transposed. Every result is rounded
 // to bf16 where torch rounds it.
 template <int STAGE>
-__global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
+__global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(1024))) char lds0[kStageBytes];
   __shared__ __attribute__((aligned(1024))) char lds1[kStageBytes];
@@ -374,13 +401,13 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
   const int cur = args.cur;
   const TileJob job = decode_tile<STAGE>(d, t - args.prefix[m], cur);
 
-  f32x16 acc[4][4];
+  f32x16 acc[kMi][kNi];
   gemm_mainloop(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl, job.R + (int64_t)job.tj * kTile * job.ldr,
                 job.ldr, job.K, st, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pbase = job.ti * kTile + (wave >> 1) * 128 + 4 * (lane >> 5);
-  const int qbase = job.tj * kTile + (wave & 1) * 128 + (lane & 31);
+  const int pbase = job.ti * kTile + (wave >> 2) * kWaveRows + 4 * (lane >> 5);
+  const int qbase = job.tj * kTile + (wave & 3) * kWaveCols + (lane & 31);
 
   // Epilogue operands are read as quads T[q][p0..p0+3] from the orientation
   // whose rows run along this lane's 4 consecutive output rows p: A is
@@ -392,7 +419,7 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
     const float s = (STAGE == ST_GRAM && args.first) ? d.scales[0] : 1.0f;
     const float cb = args.b, cc = args.c;
     const bool mirror = job.ti != job.tj;
-    u16x4 av[64];
+    u16x4 av[kQuads];
     if (STAGE == ST_POLY) load_quads(av, d.A, ldc, pbase, qbase);
     for_each_quad(acc, pbase, qbase, [&](int i, int p0, int q, const float (&x)[4]) {
       u16x4 o;
@@ -413,7 +440,7 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
     uint16_t* Xn = d.X[cur ^ 1];
     uint16_t* XTn = d.XT[cur ^ 1];
     const int64_t ldx = d.Np, ldxt = d.Mp;
-    u16x4 xv[64];
+    u16x4 xv[kQuads];
     load_quads(xv, d.XT[cur], ldxt, pbase, qbase);  // X[p][q] = Xᵀ[q][p]
     for_each_quad(acc, pbase, qbase, [&](int i, int p0, int q, const float (&x)[4]) {
       u16x4 o;
@@ -448,11 +475,12 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
   }
   auto final_bands = [&](auto* P, auto load, auto store, bool step) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      u16x4 xv[16];
-      float pv[16][4];
+    for (int mi = 0; mi < kMi; ++mi) {
+      constexpr int kBand = kNi * 4;  // quads per 32-row band
+      u16x4 xv[kBand];
+      float pv[kBand][4];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < kBand; ++j) {
         const int ni = j >> 2, g = j & 3;
         const int p0 = pbase + mi * 32 + 8 * g, q = qbase + ni * 32;
         xv[j] = *(const u16x4*)(T + (int64_t)q * ldt + p0);
@@ -465,7 +493,7 @@ __global__ __launch_bounds__(kThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) 
         }
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < kBand; ++j) {
         const int ni = j >> 2, g = j & 3;
         const int p0 = pbase + mi * 32 + 8 * g, q = qbase + ni * 32;
 #pragma unroll
