@@ -26,8 +26,6 @@ constexpr int kStages = 4;       // LDS stages in flight (4 x 32 KiB)
 constexpr int kThreads = 256;    // elementwise/prologue blocks: 4 waves of 64 lanes
 constexpr int kGemmThreads = 512;  // GEMM blocks: 8 waves, two per SIMD
 constexpr int kProTile = 64;     // prologue tile edge
-constexpr int kXcds = 8;         // MI355X: 8 XCDs, blocks dispatched round robin
-constexpr int kXcdChunk = 32;    // consecutive tiles handed to one XCD (its 32 CUs)
 
 enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
 enum Stage : int32_t { ST_GRAM = 0, ST_POLY = 1, ST_UPDATE = 2, ST_FINAL = 3 };
@@ -106,16 +104,6 @@ __device__ __forceinline__ int find_matrix(const int32_t* __restrict__ prefix, i
     if (prefix[mid] <= t) lo = mid; else hi = mid;
   }
   return lo;
-}
-
-// Block b is dispatched to XCD b % 8. Hand each XCD runs of kXcdChunk
-// consecutive tiles so tiles that share operand panels share one L2.
-__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
-  constexpr int per = kXcds * kXcdChunk;
-  const int full = (nblocks / per) * per;
-  if (b >= full) return b;
-  const int w = b % per;
-  return (b - w) + (w % kXcds) * kXcdChunk + (w / kXcds);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

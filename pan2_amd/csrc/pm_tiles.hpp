@@ -15,7 +15,22 @@ namespace pm {
 // kGroupRows row panels and 8 column panels in that XCD's L2.
 constexpr int kGroupRows = 4;
 
+constexpr int kXcds = 8;       // MI355X: 8 XCDs, blocks dispatched round robin
+constexpr int kXcdChunk = 32;  // consecutive tiles handed to one XCD (its 32 CUs)
+
 PM_HD int imin(int a, int b) { return a < b ? a : b; }
+
+// Block b is dispatched to XCD b % 8. Hand each XCD runs of kXcdChunk
+// consecutive tiles so tiles that share operand panels share one L2. A
+// permutation of [0, nblocks); blocks past the last full 256-block super-block
+// keep their index.
+PM_HD int xcd_remap(int b, int nblocks) {
+  constexpr int per = kXcds * kXcdChunk;
+  const int full = (nblocks / per) * per;
+  if (b >= full) return b;
+  const int w = b % per;
+  return (b - w) + (w % kXcds) * kXcdChunk + (w / kXcds);
+}
 
 // Rectangular np x nq tile grid; lt in [0, np*nq).
 PM_HD void full_tile(int lt, int np, int nq, int& ti, int& tj) {

@@ -96,11 +96,12 @@ def _single_tensor_muon(
         assert buf.is_contiguous() and grad.is_contiguous(), "buf and grad must be contiguous"
         assert param.shape == grad.shape, "param and update must have the same shape"
         assert param.is_contiguous(), "param and update must be contiguous"
-        if not param.is_cuda:
-            raise RuntimeError("pan2_amd Muon runs on HIP device tensors only; got a CPU parameter")
         if chunk_dim == 0:
             R, N = grad.shape
             assert R % total_chunks == 0, "# rows must be divisible by # local chunks (chunks must be same-shape)"
+        if not param.is_cuda:
+            raise RuntimeError("pan2_amd Muon runs on HIP device tensors only; got a CPU parameter")
+        if chunk_dim == 0:
             rows = R // total_chunks
             ratio = _adjust_ratio(base_adjust_lr_fn, (rows, N))
             for k in range(total_chunks):

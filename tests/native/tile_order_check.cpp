@@ -1,5 +1,6 @@
 // Host check of the GEMM tile decoders (pan2_amd/csrc/pm_tiles.hpp): every
-// work item maps to a distinct in-range tile and every tile is covered.
+// work item maps to a distinct in-range tile and every tile is covered, and
+// the XCD block remap is a permutation.
 #include <cstdio>
 #include <vector>
 
@@ -25,6 +26,15 @@ int main() {
       pm::sym_tile(lt, nt, ti, tj);
       if (ti < 0 || tj >= nt || ti > tj || seen[ti * nt + tj]++) {
         if (bad++ < 5) std::printf("sym nt=%d lt=%d -> (%d,%d)\n", nt, lt, ti, tj);
+      }
+    }
+  }
+  for (int nb = 1; nb <= 2100; nb += (nb < 600 ? 1 : 37)) {
+    std::vector<int> seen(nb, 0);
+    for (int b = 0; b < nb; ++b) {
+      const int t = pm::xcd_remap(b, nb);
+      if (t < 0 || t >= nb || seen[t]++) {
+        if (bad++ < 5) std::printf("xcd nb=%d b=%d -> %d\n", nb, b, t);
       }
     }
   }

@@ -162,3 +162,24 @@ def test_step_param_bit_exact(lr_kind):
         lr_used = float(torch.tensor(lr).item()) if lr_kind == "cpu_tensor" else lr
         ref = muon_ref.step_param(p.numpy(), u.float().numpy(), lr_used, 0.01, 1.5)
     assert np.array_equal(pd.cpu().numpy(), ref)
+
+
+def test_newton_schulz_vs_golden_torch_outputs():
+    """HIP NS on the committed golden inputs vs torch's stock bf16 NS outputs
+    (tests/golden/torch_muon_cpu.npz, written on the CPU by make_golden.py)."""
+    import os
+
+    from oracle.bf16 import from_bf16_bits
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "torch_muon_cpu.npz")
+    with np.load(path, allow_pickle=False) as z:
+        cases = sorted({k.split("/")[1] for k in z.files if k.startswith("ns/")})
+        assert cases
+        for c in cases:
+            G = z[f"ns/{c}/in"]
+            want = from_bf16_bits(z[f"ns/{c}/out_bf16"])
+            out = torch.empty(G.shape, dtype=torch.bfloat16, device=DEV)
+            _lib.newton_schulz_into([(torch.from_numpy(G).to(DEV), out)])
+            got = out.float().cpu().numpy()
+            assert rel_fro(got, want) <= 2e-2, (c, rel_fro(got, want))
+            assert rel_fro(got, muon_ref.ns_standard(G, precision="fp64")) <= 2e-2, c

@@ -1,0 +1,160 @@
+"""Host-side drop-in API (pan2_amd.optim) on the CPU: parameter split, factory
+groups, patch installation, argument errors and the host-side LR scheduler,
+against the reference's behaviour (pan/optim/muon.py, patch_muon.py,
+patch_lr_scheduler.py). No device work."""
+import pytest
+import torch
+import torch.optim._muon as torch_muon
+
+from pan2_amd.optim import patch_muon as pm
+from pan2_amd.optim.kernels import muon_momentum_nesterov
+from pan2_amd.optim.muon import (_looks_like_embedding_or_head, build_native_muon_optimizers,
+                                 split_params_for_native_muon)
+from pan2_amd.optim.patch_lr_scheduler import patch_lr_scheduler
+
+
+class Tiny(torch.nn.Module):
+    """Names cover every exclusion rule of pan/optim/muon.py:24-50."""
+
+    def __init__(self):
+        super().__init__()
+        self.embed_tokens = torch.nn.Embedding(10, 8)
+        self.patch_embed = torch.nn.Linear(8, 8)
+        self.timestep_encoder = torch.nn.Linear(8, 8)
+        self.blocks = torch.nn.ModuleList([torch.nn.ModuleDict({
+            "attn": torch.nn.Linear(8, 16),
+            "mlp": torch.nn.Linear(16, 8, bias=False),
+            "modulation": torch.nn.ModuleDict({"lin": torch.nn.Linear(8, 48)}),
+            "norm": torch.nn.LayerNorm(8),
+        })])
+        self.lm_head = torch.nn.Linear(8, 10)
+        self.frozen = torch.nn.Linear(8, 8)
+        self.frozen.requires_grad_(False)
+
+
+@pytest.fixture
+def restore_torch_muon():
+    from torch.optim.lr_scheduler import LambdaLR
+
+    saved = (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, LambdaLR.get_last_lr)
+    yield
+    torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, LambdaLR.get_last_lr = saved
+
+
+def test_exclusion_rules():
+    for name in ("embed_tokens.weight", "model.pos_embed", "lm_head.weight", "blocks.0.modulation.lin.weight",
+                 "text_modulation.weight", "timestep_encoder.0.weight", "patch_embed.proj.weight",
+                 "output_head.weight", "x.classifier.weight", "Token_Embed.w"):
+        assert _looks_like_embedding_or_head(name), name
+    for name in ("blocks.0.attn.weight", "blocks.0.mlp.weight", "decoder.out_proj.weight", "my_patch_embed.w"):
+        assert not _looks_like_embedding_or_head(name), name
+
+
+def test_split_params():
+    model = Tiny()
+    muon, adamw, stats = split_params_for_native_muon(model)
+    assert [n for n, _ in muon] == ["blocks.0.attn.weight", "blocks.0.mlp.weight"]
+    names = {n for n, _ in adamw}
+    assert "blocks.0.attn.bias" in names and "lm_head.weight" in names and "frozen.weight" not in names
+    assert stats["muon_param_tensors"] == 2
+    assert stats["muon_param_numel"] == 8 * 16 + 16 * 8
+    assert stats["trainable_param_tensors"] == len(muon) + len(adamw)
+    # 2-D weights kept on AdamW by name: embedding, patch_embed, timestep, modulation, lm_head
+    assert stats["excluded_embedding_or_head_tensors"] == 5
+
+
+def test_factory_float_lr_keeps_stock_torch(restore_torch_muon):
+    before = torch_muon._single_tensor_muon
+    out = build_native_muon_optimizers(Tiny(), lr=1e-3, weight_decay=0.05)
+    assert torch_muon._single_tensor_muon is before, "a float lr must not patch (pan/optim/muon.py:126-128)"
+    muon = out["optimizers"]["muon"]
+    assert isinstance(muon, torch.optim.Muon)
+    assert muon.defaults["adjust_lr_fn"] == "match_rms_adamw" and muon.defaults["momentum"] == 0.95
+    assert muon.defaults["weight_decay"] == 0.05
+    adamw = out["optimizers"]["adamw"]
+    assert isinstance(adamw, torch.optim.AdamW) and adamw.defaults["fused"]
+    assert adamw.defaults["betas"] == (0.95, 0.95)
+    assert out["param_names"]["muon_chunked"] == []
+
+
+def test_factory_chunk_groups_and_tensor_lr(restore_torch_muon):
+    model = Tiny()
+    lr = torch.tensor(2e-3)
+    out = build_native_muon_optimizers(model, lr=lr, muon_chunks={"blocks.0.attn.weight": (0, 2)})
+    assert torch_muon._single_tensor_muon is pm._single_tensor_muon
+    assert torch_muon._zeropower_via_newtonschulz is pm.newton_schulz
+    muon = out["optimizers"]["muon"]
+    assert len(muon.param_groups) == 2
+    assert muon.param_groups[1]["adjust_lr_fn"] == ("match_rms_adamw", 0, 2)
+    assert muon.param_groups[1]["params"][0] is model.blocks[0]["attn"].weight
+    assert out["param_names"]["muon_chunked"] == [("blocks.0.attn.weight", 0, 2)]
+    assert out["param_names"]["muon"] == ["blocks.0.mlp.weight"]
+    # the optimizer holds a clone of the tensor lr, not the caller's tensor
+    assert muon.param_groups[0]["lr"] is not lr and float(muon.param_groups[0]["lr"]) == pytest.approx(2e-3)
+
+
+def test_factory_without_trainable_params():
+    m = torch.nn.Linear(4, 4)
+    m.requires_grad_(False)
+    with pytest.raises(ValueError, match="No trainable parameters"):
+        build_native_muon_optimizers(m)
+
+
+def _call(params, grads, bufs, **kw):
+    args = dict(lr=0.02, weight_decay=0.0, momentum=0.95, nesterov=True, ns_coefficients=(3.4445, -4.775, 2.0315),
+                ns_steps=5, eps=1e-7, adjust_lr_fn=None, has_complex=False)
+    args.update(kw)
+    return pm._single_tensor_muon(params, grads, bufs, **args)
+
+
+def test_single_tensor_muon_argument_errors():
+    z = torch.zeros(4, 8)
+    with pytest.raises(ValueError):
+        _call([torch.zeros(8)], [torch.zeros(8)], [torch.zeros(8)])
+    with pytest.raises(ValueError, match="complex"):
+        _call([z], [z], [z], has_complex=True)
+    with pytest.raises(AssertionError, match="dim 1"):
+        _call([z], [z], [z], adjust_lr_fn=("match_rms_adamw", 1, 2))
+    with pytest.raises(AssertionError):
+        _call([z], [z], [z], nesterov=False)
+    with pytest.raises(AssertionError, match="divisible"):
+        _call([torch.zeros(5, 8)], [torch.zeros(5, 8)], [torch.zeros(5, 8)], adjust_lr_fn=("match_rms_adamw", 0, 2))
+    assert _call([], [], []) is None
+
+
+def test_adjust_ratio_and_scalar_lr():
+    assert pm._adjust_ratio(None, (4096, 1024)) == 2.0
+    assert pm._adjust_ratio("match_rms_adamw", (256, 1024)) == pytest.approx(6.4)
+    assert pm._scalar_lr(torch.tensor([0.5])).ndim == 0
+    assert pm._scalar_lr(0.5) == 0.5
+
+
+def test_newton_schulz_argument_errors():
+    with pytest.raises(ValueError, match="less than 100"):
+        pm.newton_schulz(torch.zeros(4, 4), (3.4445, -4.775, 2.0315), 100, 1e-7)
+    with pytest.raises(ValueError, match="2D"):
+        pm.newton_schulz(torch.zeros(4), (3.4445, -4.775, 2.0315), 5, 1e-7)
+
+
+def test_momentum_out_and_dtype_exclusive():
+    z = torch.zeros(4)
+    with pytest.raises(AssertionError, match="cannot both"):
+        muon_momentum_nesterov(z, z, 0.9, output_dtype=torch.bfloat16, out=z)
+
+
+def test_lr_scheduler_host_get_last_lr(restore_torch_muon):
+    from torch.optim.lr_scheduler import LambdaLR
+
+    p = torch.nn.Parameter(torch.zeros(2, 2))
+    opt = torch.optim.SGD([p], lr=torch.tensor(0.1))
+    sched = LambdaLR(opt, lambda e: 0.5 ** e)
+    patch_lr_scheduler()
+    for epoch in range(3):
+        got = sched.get_last_lr()
+        assert all(isinstance(v, float) for v in got)
+        assert got == [pytest.approx(0.1 * 0.5 ** epoch)]
+        opt.step()
+        sched.step()
+    # replacing base_lrs refreshes the host copy
+    sched.base_lrs = [torch.tensor(0.4)]
+    assert sched.get_last_lr() == [pytest.approx(0.4 * 0.5 ** sched.last_epoch)]
