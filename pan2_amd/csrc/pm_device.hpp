@@ -5,7 +5,7 @@
 //   pm_prologue_kernel   momentum update + bf16 X/Xᵀ write + per-tile Σx²
 //   pm_norm_kernel       per-matrix 1/‖X‖ and 1/‖X‖²
 //   pm_ns_gemm_kernel    x ns_steps x {GRAM, POLY, UPDATE|FINAL}
-// The GEMM kernel is one bf16 MFMA (v_mfma_f32_32x32x16_bf16) tile engine
+// The GEMM kernel is one bf16 MFMA (v_mfma_f32_16x16x32_bf16) tile engine
 // with four epilogues; every operand is K-contiguous ("NT" form), which is
 // why X is kept in both orientations.
 #pragma once
@@ -16,15 +16,13 @@
 namespace pm {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256;       // GEMM macro tile, rows and cols
-constexpr int kBK = 32;          // K depth of one LDS stage
-constexpr int kStages = 4;       // LDS stages in flight (4 x 32 KiB)
 constexpr int kThreads = 256;    // elementwise/prologue blocks: 4 waves of 64 lanes
-constexpr int kGemmThreads = 512;  // GEMM blocks: 8 waves, two per SIMD
+constexpr int kGemmThreads = 256;  // GEMM blocks: 4 waves, one per SIMD
 constexpr int kProTile = 64;     // prologue tile edge
 
 enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };

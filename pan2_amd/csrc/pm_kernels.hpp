@@ -104,29 +104,45 @@ __global__ __launch_bounds__(kThreads) void pm_norm_kernel(const MatDesc* descs,
 // ============================================================ GEMM engine
 //
 // C[256x256] = L[256xK] · R[256xK]ᵀ, both operands K-contiguous bf16.
-// 8 waves, two per SIMD, in a 2 (rows) x 4 (cols) grid; each owns a 128x64
-// sub-tile = 4x2 MFMA 32x32 tiles (128 fp32 accumulators per lane in AGPRs),
-// so the two waves of a SIMD take turns issuing MFMAs while the other one
-// waits on memory or the barrier.
+// 4 waves (one per SIMD) in a 2 x 2 grid, each owning a 128x128 sub-tile as
+// 8 x 8 tiles of v_mfma_f32_16x16x32_bf16 (256 fp32 accumulators per lane,
+// held in AGPRs).
 //
-// Operands stream through a kStages-deep ring of LDS stages, each holding
-// kBK = 32 columns of K for both operands (2 x 256 rows x 64 B = 32 KiB).
-// Global -> LDS copies are direct (buffer_load_dwordx4 ... lds): lane l of a
-// load writes 16 B at the instruction's LDS base + 16*l, so one instruction
-// fills 16 rows of 64 B and no VGPRs or ds_write instructions are spent on
-// staging. Each wave issues kLoadsPerWave such loads per operand per stage.
+// K advances in units of 64: a unit is 256 rows x 128 B of each operand
+// (32 KiB each), so every row an LDS-DMA load fetches is one whole 128-byte
+// cache line. Two units fit in LDS (128 KiB). Global -> LDS copies are
+// buffer_load_dwordx4 ... lds: lane l of a load writes 16 B at the
+// instruction's LDS base + 16*l, so one instruction fills 8 rows and no VGPRs
+// or ds_write instructions are spent on staging. Row chunk c (16 B) is stored
+// at chunk c ^ ((row >> 1) & 7): a ds_read_b128 phase (16 lanes, 16
+// consecutive rows, one logical chunk) then touches 16 distinct 16-byte bank
+// groups of the 64-bank LDS (measured conflict-free).
 //
-// LDS rows are 64 B (four 16-byte chunks). Chunk c of row r is stored at
-// chunk c ^ ((r >> 2) & 3): a ds_read_b128 phase serves 16 lanes reading 16
-// consecutive rows at one chunk, and this spreads them over 16 distinct
-// 16-byte bank groups of gfx950's 64-bank LDS (measured conflict-free).
-constexpr int kStageBytes = 2 * kTile * kBK * 2;   // 32 KiB
-constexpr int kOpBytes = kTile * kBK * 2;          // 16 KiB per operand
-constexpr int kWaves = kGemmThreads / 64;          // 8
-constexpr int kLoadsPerWave = kOpBytes / 1024 / kWaves;  // per operand, per stage
-constexpr int kWaveRows = 128, kWaveCols = 64;     // per-wave sub-tile
-constexpr int kMi = kWaveRows / 32, kNi = kWaveCols / 32;
-constexpr int kQuads = kMi * kNi * 4;              // accumulator quads per lane
+// A unit is 16 MFMA positions of 8 MFMAs (two k-steps of 32). Each operand
+// has its own double buffer and its own barrier:
+//   B: unit u's k-step-1 fragments are read at positions 0..7, the next
+//      unit's k-step-0 fragments at 12..15; the barrier at 12 certifies that
+//      every wave's copy of B(u+1) has landed and that no wave still reads
+//      B(u), whose buffer then receives B(u+2).
+//   A: fragments are read two positions ahead, so the next unit's first two
+//      are read at 14, 15; the barrier at 14 (after the read of A(u) at
+//      position 13 has returned) certifies A(u+1) landed and A(u) consumed.
+// Each wave issues 8 A and 8 B loads per unit, at positions 12..15 of unit u
+// and 0..5 of unit u+1 for unit u+2, and waits for exactly the loads the
+// next barrier needs (vmcnt counts them in issue order).
+//
+// MFMAs are issued from inline asm with the accumulator tied in place (the
+// compiler's own MFMA selection moves accumulators between registers across
+// the unrolled loop). An MFMA reads its sources when it executes, after
+// issue, so each fragment is kept allocated until 8 more MFMAs have issued;
+// that is what the hold() calls do. No load can then be assigned a register
+// an earlier queued MFMA still has to read.
+constexpr int kBK = 64;                        // K depth of one unit
+constexpr int kOpBytes = kTile * kBK * 2;      // 32 KiB: one operand of one unit
+constexpr int kWaveRows = 128, kWaveCols = 128;
+constexpr int kMi = kWaveRows / 16, kNi = kWaveCols / 16;  // 16x16 MFMA tiles per wave
+constexpr int kQuads = kMi * kNi;              // accumulator quads per lane
+static_assert(kGemmThreads == 256, "the GEMM engine is written for four waves");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint16_t* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
@@ -138,11 +154,17 @@ __device__ __forceinline__ lds_ptr_t to_lds(char* p) {
   return (lds_ptr_t)(__attribute__((address_space(3))) char*)p;
 }
 
-// s_waitcnt vmcnt(n), leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
+// s_waitcnt vmcnt(n) / lgkmcnt(n), leaving the other counters unconstrained
+// (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (N << 8) | (3 << 14));
 }
 
 // Block-wide barrier without the release fence of __syncthreads(), which
@@ -151,181 +173,197 @@ __device__ __forceinline__ void wait_vmcnt() {
 // accesses across it.
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// One LDS stage per __shared__ array, so the compiler's LDS-DMA tracking
-// sees that reads of one stage do not depend on copies into the others.
-struct Stages {
-  char* s[kStages];
+__device__ __forceinline__ void mfma16(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void hold(const bf16x8& v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void hold8(const bf16x8 (&v)[8]) {
+  asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+}
+
+__device__ __forceinline__ void pin16(f32x4 (&x)[kNi], f32x4 (&y)[kNi]) {
+  asm volatile("" : "+a"(x[0]), "+a"(x[1]), "+a"(x[2]), "+a"(x[3]), "+a"(x[4]), "+a"(x[5]), "+a"(x[6]), "+a"(x[7]),
+                    "+a"(y[0]), "+a"(y[1]), "+a"(y[2]), "+a"(y[3]), "+a"(y[4]), "+a"(y[5]), "+a"(y[6]), "+a"(y[7]));
+}
+
+// One __shared__ array per buffer, so the compiler's LDS-DMA tracking sees
+// that reads of one buffer do not depend on copies into the others.
+struct Ring {
+  char* a[2];
+  char* b[2];
 };
 
-// Fragments of one LDS stage (two 16-deep K steps) of this wave's sub-tile.
-struct Frags {
-  bf16x8 a[2][kMi], b[2][kNi];
+struct Engine {
+  __amdgpu_buffer_rsrc_t rl, rr;
+  int vl_off[2], vr_off[2];  // DMA lane offsets for even / odd loads
+  int frag[2];               // fragment lane offset for k-step 0 / 1
+  int aofs, bofs;            // this wave's first row (bytes) in an A / B unit
+  int ldl2, ldr2, q0;
 };
 
-// Ping-pong schedule. Waves 0-3 (group A, rows 0-127) and 4-7 (group B, rows
-// 128-255) put one wave of each group on every SIMD. Every wave runs the same
-// program, a sequence of slots closed by block barriers:
-//   M(-1) | C(0) | M(0) | C(1) | M(1) | ...
-//   C(k): the 16 MFMAs of stage k, with this wave's share of the DMA loads of
-//         stage k+3 (into buffer (k-1)%4) issued one per 4 MFMAs
-//   M(k): the LDS reads of this wave's fragments of stage k+1
-// but group B enters one slot later (one extra barrier up front, A adds one at
-// the end), so on every SIMD one wave streams MFMAs while the other reads LDS.
-// Issuing the DMA from the compute slot spreads it evenly over time: the
-// CU's vector-memory address path (about 55 B/clk measured) stays well below
-// saturation and an issue rarely blocks, whereas a burst of DMA issues at the
-// start of a memory slot made that slot, and the barrier, wait for it.
-// Ordering: stage k is read by A in slot 2k-1 and by B in slot 2k (closed by
-// lgkmcnt(0)); A's C(k+1) (slot 2k+2) and B's C(k+1) (slot 2k+3) refill its
-// buffer, after both. Each slot ends with this wave's share of the next stage
-// anyone reads waited for (k+1 after C(k), k+2 after M(k)). Stage k lives in
-// __shared__ array k % 4.
-__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, int ldl,
-                                              const uint16_t* __restrict__ Rp, int ldr,
-                                              int K, const Stages& st, f32x16 (&acc)[kMi][kNi]) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
-  const int wr = wave >> 2, wc = wave & 3;
-  const bool group_b = wr != 0;
-  const __amdgpu_buffer_rsrc_t rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
-  const __amdgpu_buffer_rsrc_t rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
-  // Load q (0..15) of an operand covers rows 16q .. 16q+15; this wave issues
-  // q = wave*kLoadsPerWave + i. Lane l fills row 16q + l/4, stored chunk l%4,
-  // i.e. logical chunk (l%4) ^ ((l/16) & 3).
-  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
-  const int vl_off = (lane >> 2) * ldl * 2 + lchunk * 16;
-  const int vr_off = (lane >> 2) * ldr * 2 + lchunk * 16;
-  const int q0 = wave * kLoadsPerWave;
-  // fragment reads: row rrow of a 32-row block, logical chunk 2*kk + kh
-  const int rrow = lane & 31, kh = lane >> 5;
-  const int rsw = (rrow >> 2) & 3;
-  const int aofs = (wr * kWaveRows + rrow) * 64;
-  const int bofs = kOpBytes + (wc * kWaveCols + rrow) * 64;
+__device__ __forceinline__ void dma_a(const Engine& e, char* dst, int unit, int i) {
+  const int q = e.q0 + i;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(e.rl, to_lds(dst + q * 1024), 16, e.vl_off[q & 1],
+                                           q * 8 * e.ldl2 + unit * kBK * 2, 0, 0);
+}
+__device__ __forceinline__ void dma_b(const Engine& e, char* dst, int unit, int i) {
+  const int q = e.q0 + i;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(e.rr, to_lds(dst + q * 1024), 16, e.vr_off[q & 1],
+                                           q * 8 * e.ldr2 + unit * kBK * 2, 0, 0);
+}
 
+// Unit u in buffer S = u % 2; REL = units after this one (2 or more: steady).
+template <int S, int REL>
+__device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine& e, f32x4 (&acc)[kMi][kNi],
+                                          bf16x8 (&bf)[2][kNi], bf16x8 (&af)[4]) {
+  const char* ca = ring.a[S];
+  const char* na = ring.a[S ^ 1];
+  const char* cb = ring.b[S];
+  const char* nb = ring.b[S ^ 1];
+  bf16x8 prev1[kNi];  // previous unit's k-step-1 fragments, still read by queued MFMAs
 #pragma unroll
-  for (int mi = 0; mi < kMi; ++mi)
+  for (int i = 0; i < kNi; ++i) prev1[i] = bf[1][i];
 #pragma unroll
-    for (int ni = 0; ni < kNi; ++ni) acc[mi][ni] = (f32x16){};
-
-  constexpr int kDma = 2 * kLoadsPerWave;  // this wave's loads per stage
-  auto issue = [&](char* dst, int kt) {
-    const int ko = kt * kBK * 2;
-#pragma unroll
-    for (int i = 0; i < kLoadsPerWave; ++i) {
-      const int q = q0 + i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, to_lds(dst + q * 1024), 16, vl_off, q * 16 * ldl * 2 + ko, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, to_lds(dst + kOpBytes + q * 1024), 16, vr_off,
-                                               q * 16 * ldr * 2 + ko, 0, 0);
+  for (int p = 0; p < 16; ++p) {
+    const int s = p / 8, mi = p % 8;
+    if (REL >= 1 && p == 12) {
+      wait_vmcnt<3>();  // B(u+1) #7 was followed by A(u+1) #5..7
+      block_barrier();
     }
-  };
-  auto read = [&](Frags& f, const char* cur) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int sw = ((2 * kk + kh) ^ rsw) << 4;
-#pragma unroll
-      for (int mi = 0; mi < kMi; ++mi) f.a[kk][mi] = *(const bf16x8*)(cur + aofs + mi * 2048 + sw);
-#pragma unroll
-      for (int ni = 0; ni < kNi; ++ni) f.b[kk][ni] = *(const bf16x8*)(cur + bofs + ni * 2048 + sw);
+    if (REL >= 1 && p == 14) {
+      if (REL >= 2) wait_vmcnt<2>(); else wait_vmcnt<0>();  // A(u+1) #7 was followed by B(u+2) #0, 1
+      wait_lgkmcnt<2>();  // the read of A(u) at position 13; only its two B reads may be pending
+      block_barrier();
     }
-  };
-  constexpr int kMfma = 0x008, kVmemRead = 0x020;
-  constexpr int kMfmas = 2 * kMi * kNi;
-  static_assert(kMfmas % kDma == 0, "DMA issues must split the MFMAs evenly");
-  // C slot: the stage's MFMAs, with `dst`'s DMA (stage kt) spread among them
-  auto compute = [&](const Frags& f, char* dst, int kt, bool refill) {
-    __builtin_amdgcn_s_setprio(1);
-    if (refill) issue(dst, kt);
+    if (p + 2 < 16) {
+      const int q = p + 2;
+      af[q % 4] = *(const bf16x8*)(ca + e.aofs + (q % 8) * 2048 + e.frag[q / 8]);
+    } else if (REL >= 1) {
+      const int q = p + 2 - 16;
+      af[q % 4] = *(const bf16x8*)(na + e.aofs + q * 2048 + e.frag[0]);
+    }
+    if (p < 8) bf[1][p] = *(const bf16x8*)(cb + e.bofs + p * 2048 + e.frag[1]);
+    if (REL >= 1 && p >= 12) {
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int mi = 0; mi < kMi; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < kNi; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[kk][mi], f.b[kk][ni], acc[mi][ni], 0, 0, 0);
-    if (refill) {
-#pragma unroll
-      for (int i = 0; i < kDma; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, kMfmas / kDma, 0);
-        __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+      for (int i = 0; i < 2; ++i) {
+        const int n = 2 * (p - 12) + i;
+        bf[0][n] = *(const bf16x8*)(nb + e.bofs + n * 2048 + e.frag[0]);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_setprio(0);
-  };
-  // this wave's DMA of a stage landed, with `pending` later stages in flight
-  auto wait_loads = [&](int pending) {
-    if (pending >= 2) wait_vmcnt<2 * kDma>();
-    else if (pending == 1) wait_vmcnt<kDma>();
-    else wait_vmcnt<0>();
-  };
-  auto slot_end = [&]() {
-    __builtin_amdgcn_sched_barrier(0);
-    block_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Every caller passes K a multiple of kTile (padded extents), so KT = K / kBK
-  // is a multiple of kStages and at least 2 * kStages.
-  static_assert(kStages == 4, "one __shared__ array per stage; schedule assumes four");
-  const int KT = K / kBK;
-  Frags f;
-
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue(st.s[s], s);
-  wait_loads(2);  // stage 0 (stages 1, 2 may stay in flight)
-  slot_end();
-  if (group_b) slot_end();  // B enters one slot later
-  // M(-1): fragments of stage 0; stage 1 landed (this wave's share)
-  read(f, st.s[0]);
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  wait_loads(1);
-  slot_end();
-
-  // Stage k in buffer s = k % 4. `refill`: stage k+3 exists (DMA'd during
-  // C(k)); `pend1` / `pend2`: stages allowed in flight after stage k+1 at the
-  // end of C(k) / after stage k+2 at the end of M(k); `next` / `next2`: stage
-  // k+1 / k+2 exists.
-  auto stage = [&](int s, int k, bool refill, int pend1, int pend2, bool next, bool next2) {
-    compute(f, st.s[(s + kStages - 1) % kStages], k + kStages - 1, refill);
-    if (next) wait_loads(pend1);
-    slot_end();
-    if (next) {
-      read(f, st.s[(s + 1) % kStages]);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): buffer (k+1)%4 read before it is refilled
-    }
-    if (next2) wait_loads(pend2);
-    slot_end();
-  };
-
-  for (int k0 = 0; k0 < KT - kStages; k0 += kStages) {
-#pragma unroll
-    for (int s = 0; s < kStages; ++s) stage(s, k0 + s, true, 2, 1, true, true);
+    for (int ni = 0; ni < kNi; ++ni) mfma16(acc[mi][ni], af[p % 4], bf[s][ni]);
+    if (REL >= 1 && p < 4) dma_b(e, ring.b[S ^ 1], u + 1, 4 + p);
+    if (REL >= 1 && p < 6) dma_a(e, ring.a[S ^ 1], u + 1, 2 + p);
+    if (REL >= 2 && p >= 12) dma_b(e, ring.b[S], u + 2, p - 12);
+    if (REL >= 2 && p >= 14) dma_a(e, ring.a[S], u + 2, p - 14);
+    hold(af[p % 4]);
+    hold(af[(p + 3) % 4]);
+    if (p == 0) hold8(prev1);
+    if (p == 8) hold8(bf[0]);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  const int k0 = KT - kStages;
-  // tail: stages issued by the end of C(k) / M(k) run to min(KT-1, k+3)
-  stage(0, k0, true, 2, 1, true, true);      // issues KT-1
-  stage(1, k0 + 1, false, 1, 0, true, true);
-  stage(2, k0 + 2, false, 0, 0, true, false);
-  stage(3, k0 + 3, false, 0, 0, false, false);
-  if (!group_b) slot_end();  // match B's extra barrier
+}
+
+// Full K loop of one tile. K must be a multiple of 256 (padded extents), so
+// the unit count KT = K / 64 is a multiple of 4.
+__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, int ldl,
+                                              const uint16_t* __restrict__ Rp, int ldr, int K, const Ring& ring,
+                                              f32x4 (&acc)[kMi][kNi]) {
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar LDS bases
+  Engine e;
+  e.rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
+  e.rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
+  e.ldl2 = ldl * 2;
+  e.ldr2 = ldr * 2;
+  // DMA load q (0..31) covers rows 8q..8q+7 of a unit; wave w issues q = 8w..8w+7.
+  // Lane l fills row 8q + l/8 at stored chunk l%8, i.e. logical chunk (l%8) ^ ((row >> 1) & 7).
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int sw = (4 * par + (lane >> 4)) & 7;
+    e.vl_off[par] = (lane >> 3) * e.ldl2 + (((lane & 7) ^ sw) << 4);
+    e.vr_off[par] = (lane >> 3) * e.ldr2 + (((lane & 7) ^ sw) << 4);
+  }
+  e.q0 = w * 8;
+  // fragment of k-step s: row l%16 of a 16-row block, logical chunk 4s + l/16
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) e.frag[s] = r16 * 128 + (((4 * s + g) ^ ((r16 >> 1) & 7)) << 4);
+  e.aofs = (w >> 1) * kWaveRows * 128;
+  e.bofs = (w & 1) * kWaveCols * 128;
+
+#pragma unroll
+  for (int i = 0; i < kMi; ++i)
+#pragma unroll
+    for (int j = 0; j < kNi; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  bf16x8 bf[2][kNi];
+  bf16x8 af[4];
+
+  // Unit 0 whole, then what a unit -1 would issue at its positions 12..15.
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma_b(e, ring.b[0], 0, i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma_a(e, ring.a[0], 0, i);
+  dma_b(e, ring.b[1], 1, 0);
+  dma_b(e, ring.b[1], 1, 1);
+  dma_b(e, ring.b[1], 1, 2);
+  dma_a(e, ring.a[1], 1, 0);
+  dma_b(e, ring.b[1], 1, 3);
+  dma_a(e, ring.a[1], 1, 1);
+  wait_vmcnt<6>();  // unit 0 landed
+  block_barrier();
+#pragma unroll
+  for (int i = 0; i < kNi; ++i) bf[0][i] = *(const bf16x8*)(ring.b[0] + e.bofs + i * 2048 + e.frag[0]);
+  af[0] = *(const bf16x8*)(ring.a[0] + e.aofs + e.frag[0]);
+  af[1] = *(const bf16x8*)(ring.a[0] + e.aofs + 2048 + e.frag[0]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // KT >= 4, so the steady loop runs at least once; a do-while keeps a single
+  // path into the last two units (no zero-trip path with other registers).
+  const int KT = K / kBK;
+  int u = 0;
+  do {
+    gemm_unit<0, 2>(ring, u, e, acc, bf, af);
+    gemm_unit<1, 2>(ring, u + 1, e, acc, bf, af);
+    u += 2;
+  } while (u < KT - 2);
+  gemm_unit<0, 1>(ring, KT - 2, e, acc, bf, af);
+  gemm_unit<1, 0>(ring, KT - 1, e, acc, bf, af);
+  // The last MFMAs must have read their sources and retired before those
+  // registers are reused and the accumulators read: the padding takes the
+  // final accumulators and fragments as operands, so nothing that touches
+  // them can be scheduled above it, and it outlasts the MFMA queue.
+  asm volatile(
+      "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
+      "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7"
+      : "+a"(acc[7][0]), "+a"(acc[7][1]), "+a"(acc[7][2]), "+a"(acc[7][3]), "+a"(acc[7][4]), "+a"(acc[7][5]),
+        "+a"(acc[7][6]), "+a"(acc[7][7]), "+a"(acc[6][4]), "+a"(acc[6][5]), "+a"(acc[6][6]), "+a"(acc[6][7])
+      : "v"(af[0]), "v"(af[1]), "v"(af[2]), "v"(af[3]), "v"(bf[1][0]), "v"(bf[1][1]), "v"(bf[1][2]), "v"(bf[1][3]),
+        "v"(bf[1][4]), "v"(bf[1][5]), "v"(bf[1][6]), "v"(bf[1][7])
+      : "memory");
+  // Every accumulator is defined here, in its AGPRs: copies the epilogue makes
+  // for VALU work cannot be hoisted into the last units (where the compiler
+  // cannot see the asm MFMAs still in flight).
+  pin16(acc[0], acc[1]);
+  pin16(acc[2], acc[3]);
+  pin16(acc[4], acc[5]);
+  asm volatile("" : "+a"(acc[6][0]), "+a"(acc[6][1]), "+a"(acc[6][2]), "+a"(acc[6][3]));
 }
 
 // Visits this lane's accumulators as quads: f(i, p0, q, x) gets rows
-// p0..p0+3 of column q, i the quad's index. (v_mfma 32x32 layout: lane l,
-// register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.) Indices are
-// compile-time after unrolling, so the accumulators stay in registers.
+// p0..p0+3 of column q, i the quad's index. (v_mfma 16x16 layout: lane l,
+// register r -> row 4*(l/16) + r, column l%16; pbase / qbase carry the lane
+// part.) Indices are compile-time after unrolling, so the accumulators stay
+// in registers.
 template <class F>
-__device__ __forceinline__ void for_each_quad(const f32x16 (&acc)[kMi][kNi], int pbase, int qbase, F&& f) {
+__device__ __forceinline__ void for_each_quad(const f32x4 (&acc)[kMi][kNi], int pbase, int qbase, F&& f) {
 #pragma unroll
   for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < kNi; ++ni)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float x[4] = {acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2],
-                            acc[mi][ni][4 * g + 3]};
-        f((mi * kNi + ni) * 4 + g, pbase + mi * 32 + 8 * g, qbase + ni * 32, x);
-      }
+    for (int ni = 0; ni < kNi; ++ni) {
+      const float x[4] = {acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]};
+      f(mi * kNi + ni, pbase + mi * 16, qbase + ni * 16, x);
+    }
 }
 
 // Loads, for every quad of this lane, the 4 consecutive elements T[q][p0..p0+3]
@@ -336,10 +374,7 @@ __device__ __forceinline__ void load_quads(u16x4 (&v)[kQuads], const uint16_t* _
   for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
     for (int ni = 0; ni < kNi; ++ni)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        v[(mi * kNi + ni) * 4 + g] =
-            *(const u16x4*)(T + (int64_t)(qbase + ni * 32) * ld + pbase + mi * 32 + 8 * g);
+      v[mi * kNi + ni] = *(const u16x4*)(T + (int64_t)(qbase + ni * 16) * ld + pbase + mi * 16);
 }
 
 // Operands and tile of one work item of stage STAGE.
@@ -388,12 +423,11 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
 template <int STAGE>
 __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(1024))) char lds0[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) char lds1[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) char lds2[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) char lds3[kStageBytes];
-  static_assert(kStages == 4, "one __shared__ array per stage");
-  const Stages st{{lds0, lds1, lds2, lds3}};
+  __shared__ __attribute__((aligned(1024))) char lds_a0[kOpBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_a1[kOpBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b0[kOpBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b1[kOpBytes];
+  const Ring ring{{lds_a0, lds_a1}, {lds_b0, lds_b1}};
 
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int m = find_matrix(args.prefix, args.n, t);
@@ -401,13 +435,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   const int cur = args.cur;
   const TileJob job = decode_tile<STAGE>(d, t - args.prefix[m], cur);
 
-  f32x16 acc[kMi][kNi];
+  f32x4 acc[kMi][kNi];
   gemm_mainloop(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl, job.R + (int64_t)job.tj * kTile * job.ldr,
-                job.ldr, job.K, st, acc);
+                job.ldr, job.K, ring, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pbase = job.ti * kTile + (wave >> 2) * kWaveRows + 4 * (lane >> 5);
-  const int qbase = job.tj * kTile + (wave & 3) * kWaveCols + (lane & 31);
+  const int pbase = job.ti * kTile + (wave >> 1) * kWaveRows + 4 * (lane >> 4);
+  const int qbase = job.tj * kTile + (wave & 1) * kWaveCols + (lane & 15);
 
   // Epilogue operands are read as quads T[q][p0..p0+3] from the orientation
   // whose rows run along this lane's 4 consecutive output rows p: A is
@@ -456,7 +490,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
 
   // ST_FINAL: P rows / Q cols are the param's own rows / cols; the a·X term
   // is X[p][q] (wide) or Xᵀ[p][q] (tall), read from the other orientation.
-  // Work goes one 32-row band (16 quads) at a time to bound register use; a
+  // Work goes one 16-row band (8 quads) at a time to bound register use; a
   // band's loads are all issued before its stores.
   const uint16_t* T = d.trans ? d.X[cur] : d.XT[cur];
   const int64_t ldt = d.trans ? d.Np : d.Mp;
@@ -476,13 +510,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   auto final_bands = [&](auto* P, auto load, auto store, bool step) {
 #pragma unroll
     for (int mi = 0; mi < kMi; ++mi) {
-      constexpr int kBand = kNi * 4;  // quads per 32-row band
+      constexpr int kBand = kNi;  // quads per 16-row band
       u16x4 xv[kBand];
       float pv[kBand][4];
 #pragma unroll
       for (int j = 0; j < kBand; ++j) {
-        const int ni = j >> 2, g = j & 3;
-        const int p0 = pbase + mi * 32 + 8 * g, q = qbase + ni * 32;
+        const int p0 = pbase + mi * 16, q = qbase + j * 16;
         xv[j] = *(const u16x4*)(T + (int64_t)q * ldt + p0);
         if (step) {
 #pragma unroll
@@ -494,12 +527,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
       }
 #pragma unroll
       for (int j = 0; j < kBand; ++j) {
-        const int ni = j >> 2, g = j & 3;
-        const int p0 = pbase + mi * 32 + 8 * g, q = qbase + ni * 32;
+        const int p0 = pbase + mi * 16, q = qbase + j * 16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int p = p0 + r;
-          const float o = bf2f(f2bf((ca * bf2f(xv[j][r]) + acc[mi][ni][4 * g + r]) * s));
+          const float o = bf2f(f2bf((ca * bf2f(xv[j][r]) + acc[mi][j][r]) * s));
           if (p < rows && q < cols) store(P + (int64_t)p * ldp + q, step ? pv[j][r] * wdf + o * neg : o);
         }
       }

@@ -181,5 +181,9 @@ def test_newton_schulz_vs_golden_torch_outputs():
             out = torch.empty(G.shape, dtype=torch.bfloat16, device=DEV)
             _lib.newton_schulz_into([(torch.from_numpy(G).to(DEV), out)])
             got = out.float().cpu().numpy()
-            assert rel_fro(got, want) <= 2e-2, (c, rel_fro(got, want))
-            assert rel_fro(got, muon_ref.ns_standard(G, precision="fp64")) <= 2e-2, c
+            exact = muon_ref.ns_standard(G, precision="fp64")
+            # the gate is against exact arithmetic; torch's bf16 output is itself
+            # up to 2e-2 from it, so two conforming results differ by <= 4e-2
+            assert rel_fro(got, exact) <= 2e-2, (c, rel_fro(got, exact))
+            assert rel_fro(want, exact) <= 2e-2, (c, "torch bf16", rel_fro(want, exact))
+            assert rel_fro(got, want) <= 4e-2, (c, rel_fro(got, want))
