@@ -248,6 +248,13 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prologue launch");
 
+  // The FINAL epilogue is compiled per param dtype; run_all keeps a group's
+  // params of one dtype (MODE_NS writes bf16).
+  const bool final_f32 = mode == MODE_STEP && items[0].desc.p_dt == PM_DTYPE_F32;
+  for (int i = 1; i < count; ++i)
+    if (mode == MODE_STEP && items[i].desc.p_dt != items[0].desc.p_dt)
+      return fail(PM_EINVAL, "internal: a group mixes param dtypes");
+
   GemmArgs ga{};
   ga.descs = ddesc;
   ga.n = count;
@@ -271,8 +278,10 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     ga.prefix = dfull;
     const bool last = it + 1 == hp->ns_steps;
     ga.stage = last ? ST_FINAL : ST_UPDATE;
-    if (last)
-      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_FINAL>, dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
+    if (last && final_f32)
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32>), dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
+    else if (last)
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16>), dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
     else
       hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
@@ -289,7 +298,9 @@ int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const floa
   if (items.empty()) return PM_OK;
   if (!workspace) return fail(PM_EINVAL, "workspace is NULL");
   if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
+  // params of one dtype together (one FINAL epilogue per launch), then longest tiles first
   std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) {
+    if (x.desc.p_dt != y.desc.p_dt) return x.desc.p_dt < y.desc.p_dt;
     return x.plan.Np != y.plan.Np ? x.plan.Np > y.plan.Np : x.plan.Mp > y.plan.Mp;
   });
   size_t i = 0;
@@ -297,6 +308,7 @@ int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const floa
   while (i < items.size()) {
     size_t j = i, need = 0;
     while (j < items.size()) {
+      if (items[j].desc.p_dt != items[i].desc.p_dt) break;  // one param dtype per group
       const size_t next = need + items[j].plan.ws;
       if (table_bytes((int)(j - i + 1)) + next > ws_bytes) break;
       need = next;

@@ -8,17 +8,67 @@ namespace pm {
 
 // ============================================================ prologue
 //
-// One 64x64 tile of X (orientation rows = short side) per block, covering the
-// padded Mp x Np extent (tiles outside the parameter write zeros).
+// One 64x64 tile of the parameter per block (tiles cover the padded extent;
+// elements outside the parameter become zeros of X).
 //   MODE_STEP: buf <- mu*buf + (1-mu)*g;  u <- (1-mu)*g + mu*buf  (nesterov)
 //              (pan/optim/muon_triton.py:44-48; fp32 math)
 //   MODE_NS:   u <- in
 // X and Xᵀ get bf16(u) (torch casts to bf16 before NS, torch/optim/_muon.py:55)
 // and partials[tile] = Σ bf16(u)², the tile's share of ‖X‖² (norm over the
 // bf16 tensor, torch/optim/_muon.py:59).
+// Each thread moves two runs of 8 consecutive elements of a row: 16-byte
+// loads and stores where the row is in range and the caller's strides and
+// bases allow, element by element otherwise. The copy in the other
+// orientation goes through an LDS tile.
+constexpr int kProPitch = kProTile + 8;  // LDS row pitch (elements), keeps 16-byte rows aligned
+
+__device__ __forceinline__ void load8(const void* base, int32_t dt, int64_t off, bool vec, bool in_row, int valid,
+                                      float (&v)[8]) {
+  if (in_row && vec && valid >= 8) {
+    if (dt == DT_F32) {
+      const f32x4 a = *(const f32x4*)((const float*)base + off);
+      const f32x4 b = *(const f32x4*)((const float*)base + off + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[4 + e] = b[e]; }
+    } else {
+      const u32x4 a = *(const u32x4*)((const uint16_t*)base + off);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf2f((uint16_t)(a[e] & 0xffff));
+        v[2 * e + 1] = bf2f((uint16_t)(a[e] >> 16));
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (in_row && e < valid) ? load_elem(base, dt, off + e) : 0.0f;
+}
+
+__device__ __forceinline__ void store8(void* base, int32_t dt, int64_t off, bool vec, int valid, const float (&v)[8]) {
+  if (vec && valid >= 8) {
+    if (dt == DT_F32) {
+      *(f32x4*)((float*)base + off) = (f32x4){v[0], v[1], v[2], v[3]};
+      *(f32x4*)((float*)base + off + 4) = (f32x4){v[4], v[5], v[6], v[7]};
+    } else {
+      u32x4 a;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = (uint32_t)f2bf(v[2 * e]) | ((uint32_t)f2bf(v[2 * e + 1]) << 16);
+      *(u32x4*)((uint16_t*)base + off) = a;
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (e < valid) store_elem(base, dt, off + e, v[e]);
+}
+
+__device__ __forceinline__ bool vec_ok(const void* base, int32_t dt, int64_t ld) {
+  return (ld % 8 == 0) && ((uintptr_t)base % 16 == 0) && (dt == DT_F32 || dt == DT_BF16);
+}
+
 __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
 #pragma clang fp contract(off)
-  __shared__ uint16_t tile[kProTile][kProTile + 2];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kProTile][kProPitch];
   __shared__ float red[kThreads / 64];
 
   const int t = blockIdx.x;
@@ -29,52 +79,72 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
   const int ti = lt / ntn, tj = lt - ti * ntn;  // tile in X coordinates
   const int pr0 = d.trans ? tj * kProTile : ti * kProTile;  // param-layout origin
   const int pc0 = d.trans ? ti * kProTile : tj * kProTile;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const float mu = args.mu, omu = 1.0f - args.mu;
+  const bool step = args.mode == MODE_STEP;
+  const bool gvec = vec_ok(d.grad, d.g_dt, d.g_ld);
+  const bool mvec = step && vec_ok(d.mom, d.m_dt, d.m_ld);
 
   float ss = 0.0f;
-#pragma unroll 4
-  for (int i = 0; i < kProTile / 4; ++i) {
-    const int r = ty + 4 * i;
-    const int pr = pr0 + r, pc = pc0 + tx;
-    float u = 0.0f;
-    if (pr < d.rows && pc < d.cols) {
-      const float g = load_elem(d.grad, d.g_dt, (int64_t)pr * d.g_ld + pc);
-      if (args.mode == MODE_STEP) {
-        const int64_t mo = (int64_t)pr * d.m_ld + pc;
-        const float m = load_elem(d.mom, d.m_dt, mo);
-        const float nm = mu * m + omu * g;
-        store_elem(d.mom, d.m_dt, mo, nm);
-        u = args.nesterov ? omu * g + mu * nm : nm;
-      } else {
-        u = g;
+  const int cg = (threadIdx.x & 7) * 8;  // first column of this thread's runs
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = (threadIdx.x >> 3) + 32 * h;
+    const int pr = pr0 + r, pc = pc0 + cg;
+    const bool in_row = pr < d.rows;
+    const int valid = d.cols - pc;  // elements of the run inside the parameter
+    float u[8];
+    float g[8];
+    load8(d.grad, d.g_dt, (int64_t)pr * d.g_ld + pc, gvec, in_row, valid, g);
+    if (step) {
+      float m[8];
+      const int64_t mo = (int64_t)pr * d.m_ld + pc;
+      load8(d.mom, d.m_dt, mo, mvec, in_row, valid, m);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float nm = mu * m[e] + omu * g[e];
+        m[e] = nm;
+        u[e] = args.nesterov ? omu * g[e] + mu * nm : nm;
       }
+      if (in_row) store8(d.mom, d.m_dt, mo, mvec, valid, m);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u[e] = g[e];
     }
-    const uint16_t ub = f2bf(u);
-    const float uf = bf2f(ub);
-    ss += uf * uf;
-    tile[r][tx] = ub;
+    u32x4 packed;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = (in_row && 2 * e < valid) ? f2bf(u[2 * e]) : (uint16_t)0;
+      const uint16_t hi = (in_row && 2 * e + 1 < valid) ? f2bf(u[2 * e + 1]) : (uint16_t)0;
+      const float flo = bf2f(lo), fhi = bf2f(hi);
+      ss += flo * flo;
+      ss += fhi * fhi;
+      packed[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    *(u32x4*)&tile[r][cg] = packed;
+    // param-layout copy: the buffer whose rows follow the param rows
+    uint16_t* dst_a = d.trans ? d.XT[0] : d.X[0];
+    const int64_t ld_a = d.trans ? d.Mp : d.Np;
+    *(u32x4*)(dst_a + (int64_t)pr * ld_a + pc) = packed;
   }
   __syncthreads();
 
-  // Param-layout copy goes to the buffer whose rows follow the param rows.
-  uint16_t* dst_a = d.trans ? d.XT[0] : d.X[0];
-  const int64_t ld_a = d.trans ? d.Mp : d.Np;
+  // other orientation: thread -> column c of the tile, rows 16*(t%4) .. +15
   uint16_t* dst_b = d.trans ? d.X[0] : d.XT[0];
   const int64_t ld_b = d.trans ? d.Np : d.Mp;
-#pragma unroll 4
-  for (int i = 0; i < kProTile / 4; ++i) {
-    const int r = ty + 4 * i;
-    dst_a[(int64_t)(pr0 + r) * ld_a + pc0 + tx] = tile[r][tx];
-  }
-#pragma unroll 4
-  for (int i = 0; i < kProTile / 4; ++i) {
-    const int c = ty + 4 * i;
-    dst_b[(int64_t)(pc0 + c) * ld_b + pr0 + tx] = tile[tx][c];
+  const int c = threadIdx.x >> 2, rb = (threadIdx.x & 3) * 16;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    u32x4 packed;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 8 * h + 2 * e;
+      packed[e] = (uint32_t)tile[r][c] | ((uint32_t)tile[r + 1][c] << 16);
+    }
+    *(u32x4*)(dst_b + (int64_t)(pc0 + c) * ld_b + pr0 + rb + 8 * h) = packed;
   }
 
   ss = wave_sum(ss);
-  if (tx == 0) red[ty] = ss;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   if (threadIdx.x == 0) d.partials[lt] = (red[0] + red[1]) + (red[2] + red[3]);
 }
@@ -394,12 +464,17 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
     j.L = j.R = d.X[cur]; j.ldl = j.ldr = d.Np; j.K = d.Np; P = Q = d.Mp; sym = true;
   } else if (STAGE == ST_POLY) {
     j.L = j.R = d.A; j.ldl = j.ldr = d.Mp; j.K = d.Mp; P = Q = d.Mp; sym = true;
-  } else if (STAGE == ST_UPDATE || !d.trans) {
+  } else if (STAGE == ST_UPDATE) {
     // C (Mp x Np) = B · X, X supplied as Xᵀ rows
     j.L = d.B; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
-  } else {
-    // tall FINAL: C (Np x Mp) = Xᵀ · B = (B X)ᵀ, already in param layout
+  } else if (!d.trans) {
+    // wide FINAL: C (Np x Mp) = Xᵀ · B = (B X)ᵀ, so a lane's quad (4 tile rows
+    // at one tile column) is 4 consecutive columns of one param row
     j.L = d.XT[cur]; j.ldl = d.Mp; j.R = d.B; j.ldr = d.Mp; j.K = d.Mp; P = d.Np; Q = d.Mp;
+  } else {
+    // tall FINAL: C (Mp x Np) = B · X, whose transpose is the param: a quad is
+    // again 4 consecutive columns of one param row
+    j.L = d.B; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
   }
   if (sym) {
     sym_tile(lt, P / kTile, j.ti, j.tj);
@@ -420,7 +495,9 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
 // GRAM and POLY are symmetric: only upper-triangle tiles are computed and
 // each off-diagonal tile is also stored transposed. Every result is rounded
 // to bf16 where torch rounds it.
-template <int STAGE>
+// PDT is the param dtype of the FINAL epilogue (one instantiation per dtype
+// keeps the epilogue's registers within budget); other stages ignore it.
+template <int STAGE, int PDT = DT_BF16>
 __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(1024))) char lds_a0[kOpBytes];
@@ -488,13 +565,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     return;
   }
 
-  // ST_FINAL: P rows / Q cols are the param's own rows / cols; the a·X term
-  // is X[p][q] (wide) or Xᵀ[p][q] (tall), read from the other orientation.
-  // Work goes one 16-row band (8 quads) at a time to bound register use; a
-  // band's loads are all issued before its stores.
-  const uint16_t* T = d.trans ? d.X[cur] : d.XT[cur];
-  const int64_t ldt = d.trans ? d.Np : d.Mp;
-  const int rows = d.rows, cols = d.cols;
+  // ST_FINAL: the tile is the param's transpose, so quad (p0..p0+3, q) is
+  // param row q, columns p0..p0+3, and its a·X term is T[q][p0..p0+3] with T
+  // the orientation of X whose rows are param rows. Loads and stores are
+  // 8-byte (bf16) or 16-byte (fp32) vectors where the param's row stride and
+  // base allow, else per element. Bands of 8 quads are software-pipelined:
+  // band mi+1's loads are issued before band mi is combined and stored.
+  const uint16_t* T = d.trans ? d.XT[cur] : d.X[cur];
+  const int64_t ldt = d.trans ? d.Mp : d.Np;
+  const int prow = d.rows, pcol = d.cols;
   const int64_t ldp = d.p_ld;
   float wdf = 0.0f, neg = 0.0f;
   if (args.mode == MODE_STEP) {
@@ -507,43 +586,84 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
       neg = d.neg_lr_host;
     }
   }
-  auto final_bands = [&](auto* P, auto load, auto store, bool step) {
+  const bool step = args.mode == MODE_STEP;
+  constexpr bool f32p = PDT == DT_F32;  // MODE_NS launches the bf16 instantiation
+  const int vec_align = f32p ? 16 : 8;
+  const bool vec = (ldp % 4 == 0) && ((uintptr_t)d.param % vec_align == 0);
+  constexpr int kBand = kNi;  // quads of one 16-row band: 8 param rows x 4 columns
+  u16x4 xv[2][kBand];
+  float pv[2][kBand][4];
+  auto load_band = [&](int mi, u16x4 (&x)[kBand], float (&pp)[kBand][4]) {
 #pragma unroll
-    for (int mi = 0; mi < kMi; ++mi) {
-      constexpr int kBand = kNi;  // quads per 16-row band
-      u16x4 xv[kBand];
-      float pv[kBand][4];
+    for (int j = 0; j < kBand; ++j) {
+      const int c0 = pbase + mi * 16, r = qbase + j * 16;  // param row r, columns c0..c0+3
+      x[j] = *(const u16x4*)(T + (int64_t)r * ldt + c0);
+      if (!step) continue;
+      const bool full = vec && r < prow && c0 + 3 < pcol;
+      if (f32p) {
+        const float* src = (const float*)d.param + (int64_t)r * ldp + c0;
+        if (full) {
+          const f32x4 v = *(const f32x4*)src;
 #pragma unroll
-      for (int j = 0; j < kBand; ++j) {
-        const int p0 = pbase + mi * 16, q = qbase + j * 16;
-        xv[j] = *(const u16x4*)(T + (int64_t)q * ldt + p0);
-        if (step) {
+          for (int e = 0; e < 4; ++e) pp[j][e] = v[e];
+        } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int p = p0 + r;
-            pv[j][r] = (p < rows && q < cols) ? load(P + (int64_t)p * ldp + q) : 0.0f;
-          }
+          for (int e = 0; e < 4; ++e) pp[j][e] = (r < prow && c0 + e < pcol) ? src[e] : 0.0f;
         }
-      }
+      } else {
+        const uint16_t* src = (const uint16_t*)d.param + (int64_t)r * ldp + c0;
+        if (full) {
+          const u16x4 v = *(const u16x4*)src;
 #pragma unroll
-      for (int j = 0; j < kBand; ++j) {
-        const int p0 = pbase + mi * 16, q = qbase + j * 16;
+          for (int e = 0; e < 4; ++e) pp[j][e] = bf2f(v[e]);
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int p = p0 + r;
-          const float o = bf2f(f2bf((ca * bf2f(xv[j][r]) + acc[mi][j][r]) * s));
-          if (p < rows && q < cols) store(P + (int64_t)p * ldp + q, step ? pv[j][r] * wdf + o * neg : o);
+          for (int e = 0; e < 4; ++e) pp[j][e] = (r < prow && c0 + e < pcol) ? bf2f(src[e]) : 0.0f;
         }
       }
     }
   };
-  auto ld_f32 = [](const float* a) { return *a; };
-  auto st_f32 = [](float* a, float v) { *a = v; };
-  auto ld_bf16 = [](const uint16_t* a) { return bf2f(*a); };
-  auto st_bf16 = [](uint16_t* a, float v) { *a = f2bf(v); };
-  if (args.mode == MODE_NS) final_bands((uint16_t*)d.param, ld_bf16, st_bf16, false);
-  else if (d.p_dt == DT_F32) final_bands((float*)d.param, ld_f32, st_f32, true);
-  else final_bands((uint16_t*)d.param, ld_bf16, st_bf16, true);
+  auto store_band = [&](int mi, const u16x4 (&x)[kBand], const float (&pp)[kBand][4]) {
+#pragma unroll
+    for (int j = 0; j < kBand; ++j) {
+      const int c0 = pbase + mi * 16, r = qbase + j * 16;
+      if (r >= prow) continue;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float on = bf2f(f2bf((ca * bf2f(x[j][e]) + acc[mi][j][e]) * s));  // bf16 orthogonalised update
+        o[e] = step ? pp[j][e] * wdf + on * neg : on;
+      }
+      const bool full = vec && c0 + 3 < pcol;
+      if (f32p) {
+        float* dst = (float*)d.param + (int64_t)r * ldp + c0;
+        if (full) {
+          *(f32x4*)dst = (f32x4){o[0], o[1], o[2], o[3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (c0 + e < pcol) dst[e] = o[e];
+        }
+      } else {
+        uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
+        if (full) {
+          *(u16x4*)dst = (u16x4){f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (c0 + e < pcol) dst[e] = f2bf(o[e]);
+        }
+      }
+    }
+  };
+  load_band(0, xv[0], pv[0]);
+#pragma unroll
+  for (int mi = 0; mi < kMi; ++mi) {
+    // one band per scheduling region, so bands are not interleaved (register pressure)
+    __builtin_amdgcn_sched_barrier(0);
+    if (mi + 1 < kMi) load_band(mi + 1, xv[(mi + 1) & 1], pv[(mi + 1) & 1]);
+    store_band(mi, xv[mi & 1], pv[mi & 1]);
+  }
 }
 
 // ============================================================ elementwise

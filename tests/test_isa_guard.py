@@ -1,0 +1,76 @@
+"""Static checks of the GEMM kernels' gfx950 assembly (CPU only; hipcc -S).
+
+The GEMM engine issues its MFMAs from inline asm with the accumulators tied
+in AGPRs, so the compiler does not know their latency. Three things would
+then corrupt results silently, and none may appear in any GEMM instantiation:
+  * scratch traffic (a spill of an accumulator right after its MFMA reads a
+    stale value, and spills of anything cost bandwidth),
+  * accumulator copies (v_accvgpr_read/write/mov) between the first and the
+    last MFMA,
+  * a load whose destination is a source register of one of the previous 8
+    MFMAs inside the MFMA region (an MFMA reads its sources when it executes,
+    after issue).
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "pan2_amd", "csrc", "panmuon.hip")
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+
+@pytest.fixture(scope="module")
+def gemm_kernels(tmp_path_factory):
+    if not os.path.exists(HIPCC):
+        pytest.skip("needs hipcc")
+    out = tmp_path_factory.mktemp("isa") / "panmuon.s"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+                    "-packed-fp32-ops", "--cuda-device-only", "-S", SRC, "-o", str(out)],
+                   check=True, capture_output=True)
+    asm = out.read_text()
+    kernels = {}
+    for m in re.finditer(r"^(_ZN2pm17pm_ns_gemm_kernel\w+):.*$", asm, flags=re.M):
+        body = asm[m.end():]
+        kernels[m.group(1)] = body[:body.index("s_endpgm")].split("\n")
+    assert len(kernels) == 5, sorted(kernels)  # GRAM, POLY, UPDATE, FINAL x {f32, bf16}
+    return kernels
+
+
+def _regs(tok):
+    m = re.match(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def test_no_scratch(gemm_kernels):
+    for name, lines in gemm_kernels.items():
+        n = sum(1 for ln in lines if "scratch_" in ln)
+        assert n == 0, f"{name}: {n} scratch instructions"
+
+
+def test_no_accumulator_copies_between_mfmas(gemm_kernels):
+    for name, lines in gemm_kernels.items():
+        idx = [i for i, ln in enumerate(lines) if "v_mfma" in ln]
+        copies = [ln.strip() for ln in lines[idx[0]:idx[-1]] if "v_accvgpr" in ln]
+        assert not copies, f"{name}: {len(copies)} accumulator copies in the MFMA region, e.g. {copies[:2]}"
+
+
+def test_loads_do_not_overwrite_queued_mfma_sources(gemm_kernels):
+    for name, lines in gemm_kernels.items():
+        idx = [i for i, ln in enumerate(lines) if "v_mfma" in ln]
+        recent = []
+        for ln in lines[idx[0]:idx[-1] + 1]:
+            t = ln.strip()
+            if t.startswith("v_mfma"):
+                ops = [o.strip() for o in t.split(None, 1)[1].split(",")]
+                recent = (recent + [_regs(ops[1]) | _regs(ops[2])])[-8:]
+            elif t.startswith("ds_read") or t.startswith("global_load") or (
+                    t.startswith("buffer_load") and " lds" not in t):
+                dst = _regs(t.split(None, 1)[1].split(",")[0].strip())
+                assert not any(dst & src for src in recent), f"{name}: {t}"
