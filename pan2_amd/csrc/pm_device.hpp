@@ -22,7 +22,7 @@ typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256;       // GEMM macro tile, rows and cols
 constexpr int kThreads = 256;    // elementwise/prologue blocks: 4 waves of 64 lanes
-constexpr int kGemmThreads = 256;  // GEMM blocks: 4 waves, one per SIMD
+constexpr int kGemmThreads = 512;  // GEMM blocks: 8 waves, two per SIMD
 constexpr int kProTile = 64;     // prologue tile edge
 
 enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };

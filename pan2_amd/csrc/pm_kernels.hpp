@@ -174,9 +174,9 @@ __global__ __launch_bounds__(kThreads) void pm_norm_kernel(const MatDesc* descs,
 // ============================================================ GEMM engine
 //
 // C[256x256] = L[256xK] · R[256xK]ᵀ, both operands K-contiguous bf16.
-// 4 waves (one per SIMD) in a 2 x 2 grid, each owning a 128x128 sub-tile as
-// 8 x 8 tiles of v_mfma_f32_16x16x32_bf16 (256 fp32 accumulators per lane,
-// held in AGPRs).
+// 8 waves (two per SIMD, so one issues MFMAs while the other waits) in a
+// 2 x 4 grid, each owning a 128x64 sub-tile as 8 x 4 tiles of
+// v_mfma_f32_16x16x32_bf16 (128 fp32 accumulators per lane, held in AGPRs).
 //
 // K advances in units of 64: a unit is 256 rows x 128 B of each operand
 // (32 KiB each), so every row an LDS-DMA load fetches is one whole 128-byte
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void pm_norm_kernel(const MatDesc* descs,
 // consecutive rows, one logical chunk) then touches 16 distinct 16-byte bank
 // groups of the 64-bank LDS (measured conflict-free).
 //
-// A unit is 16 MFMA positions of 8 MFMAs (two k-steps of 32). Each operand
+// A unit is 16 MFMA positions of 4 MFMAs (two k-steps of 32). Each operand
 // has its own double buffer and its own barrier:
 //   B: unit u's k-step-1 fragments are read at positions 0..7, the next
 //      unit's k-step-0 fragments at 12..15; the barrier at 12 certifies that
@@ -197,22 +197,22 @@ __global__ __launch_bounds__(kThreads) void pm_norm_kernel(const MatDesc* descs,
 //   A: fragments are read two positions ahead, so the next unit's first two
 //      are read at 14, 15; the barrier at 14 (after the read of A(u) at
 //      position 13 has returned) certifies A(u+1) landed and A(u) consumed.
-// Each wave issues 8 A and 8 B loads per unit, at positions 12..15 of unit u
-// and 0..5 of unit u+1 for unit u+2, and waits for exactly the loads the
-// next barrier needs (vmcnt counts them in issue order).
+// Each wave issues 4 A and 4 B loads per unit for unit u+2: B at positions
+// 12..15 and A at 14, 15 of unit u and 0, 1 of unit u+1; it waits for exactly
+// the loads the next barrier needs (vmcnt counts them in issue order).
 //
 // MFMAs are issued from inline asm with the accumulator tied in place (the
 // compiler's own MFMA selection moves accumulators between registers across
 // the unrolled loop). An MFMA reads its sources when it executes, after
-// issue, so each fragment is kept allocated until 8 more MFMAs have issued;
-// that is what the hold() calls do. No load can then be assigned a register
+// issue, so each fragment is kept allocated until 8 more MFMAs (two
+// positions) have issued; that is what the hold() calls do. No load can then be assigned a register
 // an earlier queued MFMA still has to read.
 constexpr int kBK = 64;                        // K depth of one unit
 constexpr int kOpBytes = kTile * kBK * 2;      // 32 KiB: one operand of one unit
-constexpr int kWaveRows = 128, kWaveCols = 128;
+constexpr int kWaveRows = 128, kWaveCols = 64;
 constexpr int kMi = kWaveRows / 16, kNi = kWaveCols / 16;  // 16x16 MFMA tiles per wave
 constexpr int kQuads = kMi * kNi;              // accumulator quads per lane
-static_assert(kGemmThreads == 256, "the GEMM engine is written for four waves");
+static_assert(kGemmThreads == 512, "the GEMM engine is written for eight waves");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint16_t* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
@@ -247,13 +247,12 @@ __device__ __forceinline__ void mfma16(f32x4& acc, const bf16x8& a, const bf16x8
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 __device__ __forceinline__ void hold(const bf16x8& v) { asm volatile("" ::"v"(v)); }
-__device__ __forceinline__ void hold8(const bf16x8 (&v)[8]) {
-  asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
+__device__ __forceinline__ void hold4(const bf16x8 (&v)[4]) {
+  asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
 }
 
-__device__ __forceinline__ void pin16(f32x4 (&x)[kNi], f32x4 (&y)[kNi]) {
-  asm volatile("" : "+a"(x[0]), "+a"(x[1]), "+a"(x[2]), "+a"(x[3]), "+a"(x[4]), "+a"(x[5]), "+a"(x[6]), "+a"(x[7]),
-                    "+a"(y[0]), "+a"(y[1]), "+a"(y[2]), "+a"(y[3]), "+a"(y[4]), "+a"(y[5]), "+a"(y[6]), "+a"(y[7]));
+__device__ __forceinline__ void pin8(f32x4 (&x)[kNi], f32x4 (&y)[kNi]) {
+  asm volatile("" : "+a"(x[0]), "+a"(x[1]), "+a"(x[2]), "+a"(x[3]), "+a"(y[0]), "+a"(y[1]), "+a"(y[2]), "+a"(y[3]));
 }
 
 // One __shared__ array per buffer, so the compiler's LDS-DMA tracking sees
@@ -285,7 +284,7 @@ __device__ __forceinline__ void dma_b(const Engine& e, char* dst, int unit, int 
 // Unit u in buffer S = u % 2; REL = units after this one (2 or more: steady).
 template <int S, int REL>
 __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine& e, f32x4 (&acc)[kMi][kNi],
-                                          bf16x8 (&bf)[2][kNi], bf16x8 (&af)[4]) {
+                                          bf16x8 (&bf)[2][kNi], bf16x8 (&af)[8]) {
   const char* ca = ring.a[S];
   const char* na = ring.a[S ^ 1];
   const char* cb = ring.b[S];
@@ -297,39 +296,34 @@ __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine&
   for (int p = 0; p < 16; ++p) {
     const int s = p / 8, mi = p % 8;
     if (REL >= 1 && p == 12) {
-      wait_vmcnt<3>();  // B(u+1) #7 was followed by A(u+1) #5..7
+      wait_vmcnt<3>();  // B(u+1) #3 (position 15 of u-1) was followed by A(u+1) #1, #2, #3
       block_barrier();
     }
     if (REL >= 1 && p == 14) {
-      if (REL >= 2) wait_vmcnt<2>(); else wait_vmcnt<0>();  // A(u+1) #7 was followed by B(u+2) #0, 1
-      wait_lgkmcnt<2>();  // the read of A(u) at position 13; only its two B reads may be pending
+      if (REL >= 2) wait_vmcnt<2>(); else wait_vmcnt<0>();  // A(u+1) #3 (position 1) was followed by B(u+2) #0, 1
+      wait_lgkmcnt<2>();  // the read of A(u) at position 13; only the B reads of 13 and 14 may be pending
       block_barrier();
     }
     if (p + 2 < 16) {
       const int q = p + 2;
-      af[q % 4] = *(const bf16x8*)(ca + e.aofs + (q % 8) * 2048 + e.frag[q / 8]);
+      af[q % 8] = *(const bf16x8*)(ca + e.aofs + (q % 8) * 2048 + e.frag[q / 8]);
     } else if (REL >= 1) {
       const int q = p + 2 - 16;
-      af[q % 4] = *(const bf16x8*)(na + e.aofs + q * 2048 + e.frag[0]);
+      af[q % 8] = *(const bf16x8*)(na + e.aofs + q * 2048 + e.frag[0]);
     }
-    if (p < 8) bf[1][p] = *(const bf16x8*)(cb + e.bofs + p * 2048 + e.frag[1]);
-    if (REL >= 1 && p >= 12) {
+    if (p < kNi) bf[1][p] = *(const bf16x8*)(cb + e.bofs + p * 2048 + e.frag[1]);
+    if (REL >= 1 && p >= 12) bf[0][p - 12] = *(const bf16x8*)(nb + e.bofs + (p - 12) * 2048 + e.frag[0]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int n = 2 * (p - 12) + i;
-        bf[0][n] = *(const bf16x8*)(nb + e.bofs + n * 2048 + e.frag[0]);
-      }
-    }
-#pragma unroll
-    for (int ni = 0; ni < kNi; ++ni) mfma16(acc[mi][ni], af[p % 4], bf[s][ni]);
-    if (REL >= 1 && p < 4) dma_b(e, ring.b[S ^ 1], u + 1, 4 + p);
-    if (REL >= 1 && p < 6) dma_a(e, ring.a[S ^ 1], u + 1, 2 + p);
+    for (int ni = 0; ni < kNi; ++ni) mfma16(acc[mi][ni], af[p % 8], bf[s][ni]);
+    if (REL >= 1 && p < 2) dma_a(e, ring.a[S ^ 1], u + 1, 2 + p);
     if (REL >= 2 && p >= 12) dma_b(e, ring.b[S], u + 2, p - 12);
     if (REL >= 2 && p >= 14) dma_a(e, ring.a[S], u + 2, p - 14);
-    hold(af[p % 4]);
-    hold(af[(p + 3) % 4]);
-    if (p == 0) hold8(prev1);
-    if (p == 8) hold8(bf[0]);
+    // a fragment stays allocated through two positions (8 MFMAs) after its last use
+    hold(af[p % 8]);
+    hold(af[(p + 7) % 8]);
+    hold(af[(p + 6) % 8]);
+    if (p <= 2) hold4(prev1);
+    if (p >= 8 && p <= 10) hold4(bf[0]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -346,7 +340,7 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
   e.rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
   e.ldl2 = ldl * 2;
   e.ldr2 = ldr * 2;
-  // DMA load q (0..31) covers rows 8q..8q+7 of a unit; wave w issues q = 8w..8w+7.
+  // DMA load q (0..31) covers rows 8q..8q+7 of a unit; wave w issues q = 4w..4w+3.
   // Lane l fills row 8q + l/8 at stored chunk l%8, i.e. logical chunk (l%8) ^ ((row >> 1) & 7).
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
@@ -354,26 +348,26 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
     e.vl_off[par] = (lane >> 3) * e.ldl2 + (((lane & 7) ^ sw) << 4);
     e.vr_off[par] = (lane >> 3) * e.ldr2 + (((lane & 7) ^ sw) << 4);
   }
-  e.q0 = w * 8;
+  e.q0 = w * 4;
   // fragment of k-step s: row l%16 of a 16-row block, logical chunk 4s + l/16
   const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int s = 0; s < 2; ++s) e.frag[s] = r16 * 128 + (((4 * s + g) ^ ((r16 >> 1) & 7)) << 4);
-  e.aofs = (w >> 1) * kWaveRows * 128;
-  e.bofs = (w & 1) * kWaveCols * 128;
+  e.aofs = (w >> 2) * kWaveRows * 128;
+  e.bofs = (w & 3) * kWaveCols * 128;
 
 #pragma unroll
   for (int i = 0; i < kMi; ++i)
 #pragma unroll
     for (int j = 0; j < kNi; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
   bf16x8 bf[2][kNi];
-  bf16x8 af[4];
+  bf16x8 af[8];
 
   // Unit 0 whole, then what a unit -1 would issue at its positions 12..15.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_b(e, ring.b[0], 0, i);
+  for (int i = 0; i < 4; ++i) dma_b(e, ring.b[0], 0, i);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_a(e, ring.a[0], 0, i);
+  for (int i = 0; i < 4; ++i) dma_a(e, ring.a[0], 0, i);
   dma_b(e, ring.b[1], 1, 0);
   dma_b(e, ring.b[1], 1, 1);
   dma_b(e, ring.b[1], 1, 2);
@@ -406,18 +400,16 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
   asm volatile(
       "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n"
       "s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7"
-      : "+a"(acc[7][0]), "+a"(acc[7][1]), "+a"(acc[7][2]), "+a"(acc[7][3]), "+a"(acc[7][4]), "+a"(acc[7][5]),
-        "+a"(acc[7][6]), "+a"(acc[7][7]), "+a"(acc[6][4]), "+a"(acc[6][5]), "+a"(acc[6][6]), "+a"(acc[6][7])
-      : "v"(af[0]), "v"(af[1]), "v"(af[2]), "v"(af[3]), "v"(bf[1][0]), "v"(bf[1][1]), "v"(bf[1][2]), "v"(bf[1][3]),
-        "v"(bf[1][4]), "v"(bf[1][5]), "v"(bf[1][6]), "v"(bf[1][7])
+      : "+a"(acc[7][0]), "+a"(acc[7][1]), "+a"(acc[7][2]), "+a"(acc[7][3]), "+a"(acc[6][0]), "+a"(acc[6][1]),
+        "+a"(acc[6][2]), "+a"(acc[6][3])
+      : "v"(af[13 % 8]), "v"(af[14 % 8]), "v"(af[15 % 8]), "v"(bf[1][0]), "v"(bf[1][1]), "v"(bf[1][2]), "v"(bf[1][3])
       : "memory");
   // Every accumulator is defined here, in its AGPRs: copies the epilogue makes
   // for VALU work cannot be hoisted into the last units (where the compiler
   // cannot see the asm MFMAs still in flight).
-  pin16(acc[0], acc[1]);
-  pin16(acc[2], acc[3]);
-  pin16(acc[4], acc[5]);
-  asm volatile("" : "+a"(acc[6][0]), "+a"(acc[6][1]), "+a"(acc[6][2]), "+a"(acc[6][3]));
+  pin8(acc[0], acc[1]);
+  pin8(acc[2], acc[3]);
+  pin8(acc[4], acc[5]);
 }
 
 // Visits this lane's accumulators as quads: f(i, p0, q, x) gets rows
@@ -517,8 +509,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
                 job.ldr, job.K, ring, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pbase = job.ti * kTile + (wave >> 1) * kWaveRows + 4 * (lane >> 4);
-  const int qbase = job.tj * kTile + (wave & 1) * kWaveCols + (lane & 15);
+  const int pbase = job.ti * kTile + (wave >> 2) * kWaveRows + 4 * (lane >> 4);
+  const int qbase = job.tj * kTile + (wave & 3) * kWaveCols + (lane & 15);
 
   // Epilogue operands are read as quads T[q][p0..p0+3] from the orientation
   // whose rows run along this lane's 4 consecutive output rows p: A is
@@ -590,7 +582,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   constexpr bool f32p = PDT == DT_F32;  // MODE_NS launches the bf16 instantiation
   const int vec_align = f32p ? 16 : 8;
   const bool vec = (ldp % 4 == 0) && ((uintptr_t)d.param % vec_align == 0);
-  constexpr int kBand = kNi;  // quads of one 16-row band: 8 param rows x 4 columns
+  constexpr int kBand = kNi;  // quads of one 16-row band: kNi param rows x 4 columns
   u16x4 xv[2][kBand];
   float pv[2][kBand][4];
   auto load_band = [&](int mi, u16x4 (&x)[kBand], float (&pp)[kBand][4]) {
