@@ -69,6 +69,68 @@ def build_state(shapes, config, device, seed=1234):
     return params, moms
 
 
+GEMM_KERNEL = "pm_ns_gemm_kernel"
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def traffic_path(workload: str) -> str:
+    return os.path.join(ROOT, "profiles", f"{GEMM_KERNEL}_{workload}_traffic.json")
+
+
+def traffic_bytes(workload: str):
+    """HBM bytes per GEMM launch from the committed counter summary, or None."""
+    path = traffic_path(workload)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["bytes_per_launch"]
+
+
+def _counter_by_dispatch(path: str, counter: str) -> dict:
+    import csv
+
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (r["Dispatch_Id"], r["Kernel_Name"])
+            out[key] = out.get(key, 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def traffic_summary(args) -> int:
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the GEMM launches, each
+    scaled by what the same counter reads for the calibration copy (copy_mib MiB
+    read and written). Writes the JSON that bench.py reports as traffic."""
+    if not (args.fetch_csv and args.write_csv and args.copy_mib):
+        print("--traffic-summary needs --fetch-csv, --write-csv and --copy-mib", file=sys.stderr)
+        return 2
+    known_kib = args.copy_mib * 1024.0
+    result = {}
+    for counter, path in (("FETCH_SIZE", args.fetch_csv), ("WRITE_SIZE", args.write_csv)):
+        vals = _counter_by_dispatch(path, counter)
+        # the calibration copies are the large copy dispatches (the counter may
+        # read a fixed fraction of the bytes: that fraction is the scale)
+        copies = [v for (d, k), v in vals.items() if COPY_KERNEL in k and v >= 0.25 * known_kib]
+        gemm = [v for (d, k), v in vals.items() if GEMM_KERNEL in k]
+        if not copies or not gemm:
+            print(f"{counter}: no calibration copy or no GEMM dispatches in {path}", file=sys.stderr)
+            return 1
+        copy_kib = sum(copies) / len(copies)
+        scale = known_kib / copy_kib
+        result[counter] = {"copy_kib": copy_kib, "scale": scale, "gemm_launches": len(gemm),
+                           "gemm_kib_mean_raw": sum(gemm) / len(gemm),
+                           "gemm_bytes_mean": sum(gemm) / len(gemm) * scale * 1024.0}
+    out = {"kernel": GEMM_KERNEL, "copy_mib": args.copy_mib,
+           "bytes_per_launch": result["FETCH_SIZE"]["gemm_bytes_mean"] + result["WRITE_SIZE"]["gemm_bytes_mean"],
+           "fetch": result["FETCH_SIZE"], "write": result["WRITE_SIZE"]}
+    with open(args.traffic_summary, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,7 +140,16 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workspace-gib", type=float, default=0.0, help="libpanmuon workspace cap (0 = default)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after timing, run a plain device copy of this many MiB 3x (HBM counter calibration)")
+    ap.add_argument("--traffic-summary", metavar="OUT_JSON",
+                    help="offline: turn rocprofv3 FETCH_SIZE / WRITE_SIZE CSVs of a --copy-mib run into HBM bytes "
+                         "per GEMM launch (needs --fetch-csv, --write-csv, --copy-mib)")
+    ap.add_argument("--fetch-csv")
+    ap.add_argument("--write-csv")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU sharding is a design, not code", file=sys.stderr)
@@ -124,6 +195,14 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     recs = _lib.timing_read()
     _lib.timing_enable(False)
+    if args.copy_mib:
+        # HBM counter calibration: a copy kernel that reads and writes exactly copy_mib MiB
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     ms_per_step = elapsed * 1e3 / args.steps
     print(f"bench: {ms_per_step:.2f} ms/step", file=sys.stderr, flush=True)
 
@@ -203,7 +282,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(name),
             "launches": len(gemm),
             "avg_launch_ms": round(gemm_ms / max(1, len(gemm)), 3),
         },
