@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -72,9 +73,30 @@ Plan make_plan(int64_t rows, int64_t cols) {
   return p;
 }
 
-// Descriptor table layout: descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1]
-size_t table_bytes(int n) {
-  return align_up((size_t)n * sizeof(MatDesc)) + 3 * align_up((size_t)(n + 1) * 4);
+// GEMM launches of one group: GRAM, POLY and UPDATE/FINAL per iteration.
+int gemm_launches(const pm_hparams* hp) { return 3 * hp->ns_steps; }
+
+// Descriptor table layout:
+//   descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1] | queues[launches][kXcds]
+// The queue counters are uploaded as zeros with the rest of the table, so
+// every GEMM launch starts with empty counters without a memset.
+size_t table_bytes(int n, int launches) {
+  return align_up((size_t)n * sizeof(MatDesc)) + 3 * align_up((size_t)(n + 1) * 4) +
+         align_up((size_t)launches * kXcds * 4);
+}
+
+// Persistent GEMM grid: one block per CU (the kernel's LDS allows no more),
+// never more blocks than tiles.
+int gemm_grid(int tiles) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return std::max(1, std::min(tiles, n));
 }
 
 bool valid_dtype(int32_t dt) { return dt == PM_DTYPE_F32 || dt == PM_DTYPE_BF16; }
@@ -187,13 +209,14 @@ void timing_mark(hipStream_t stream, int kind, int group, int iteration, int nma
 int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
               double lr_host, char* ws, hipStream_t stream) {
   // Table first, then per-matrix buffers.
-  const size_t tb = table_bytes(count);
+  const size_t tb = table_bytes(count, gemm_launches(hp));
   char* cursor = ws + tb;
   std::vector<char> host(tb, 0);
   MatDesc* descs = (MatDesc*)host.data();
   int32_t* pro = (int32_t*)(host.data() + align_up((size_t)count * sizeof(MatDesc)));
   int32_t* sym = (int32_t*)((char*)pro + align_up((size_t)(count + 1) * 4));
   int32_t* full = (int32_t*)((char*)sym + align_up((size_t)(count + 1) * 4));
+  const int32_t* queues = (const int32_t*)((char*)full + align_up((size_t)(count + 1) * 4));  // zeros
   pro[0] = sym[0] = full[0] = 0;
   for (int i = 0; i < count; ++i) {
     Item& it = items[i];
@@ -239,6 +262,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   const int32_t* dpro = (const int32_t*)(ws + ((char*)pro - host.data()));
   const int32_t* dsym = (const int32_t*)(ws + ((char*)sym - host.data()));
   const int32_t* dfull = (const int32_t*)(ws + ((char*)full - host.data()));
+  int32_t* dqueues = (int32_t*)(ws + ((const char*)queues - host.data()));
 
   ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov};
   hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
@@ -262,6 +286,8 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   ga.lr_dev = lr_dev;
   ga.wd = (float)hp->weight_decay;
   ga.wdf_host = (float)(1.0 - lr_host * (double)hp->weight_decay);
+  const int sym_grid = gemm_grid(sym[count]), full_grid = gemm_grid(full[count]);
+  int launch = 0;  // queue counters: one set of kXcds per launch
   for (int it = 0; it < hp->ns_steps; ++it) {
     Coeff k{hp->a, hp->b, hp->c};
     if (hp->coeffs) k = Coeff{hp->coeffs[3 * it], hp->coeffs[3 * it + 1], hp->coeffs[3 * it + 2]};
@@ -269,21 +295,26 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     ga.cur = it & 1;
     ga.first = it == 0;
     ga.prefix = dsym;
+    ga.total = sym[count];
     ga.stage = ST_GRAM;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[count]), dim3(kGemmThreads), 0, stream, ga);
+    ga.queues = dqueues + kXcds * launch++;
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
     ga.stage = ST_POLY;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_POLY>, dim3(sym[count]), dim3(kGemmThreads), 0, stream, ga);
+    ga.queues = dqueues + kXcds * launch++;
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_POLY>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, PM_K_POLY, group, it, count, f_poly, 0.0);
     ga.prefix = dfull;
+    ga.total = full[count];
     const bool last = it + 1 == hp->ns_steps;
     ga.stage = last ? ST_FINAL : ST_UPDATE;
+    ga.queues = dqueues + kXcds * launch++;
     if (last && final_f32)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32>), dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32>), dim3(full_grid), dim3(kGemmThreads), 0, stream, ga);
     else if (last)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16>), dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16>), dim3(full_grid), dim3(kGemmThreads), 0, stream, ga);
     else
-      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full[count]), dim3(kGemmThreads), 0, stream, ga);
+      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full_grid), dim3(kGemmThreads), 0, stream, ga);
     timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "Newton-Schulz launch");
@@ -310,13 +341,13 @@ int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const floa
     while (j < items.size()) {
       if (items[j].desc.p_dt != items[i].desc.p_dt) break;  // one param dtype per group
       const size_t next = need + items[j].plan.ws;
-      if (table_bytes((int)(j - i + 1)) + next > ws_bytes) break;
+      if (table_bytes((int)(j - i + 1), gemm_launches(hp)) + next > ws_bytes) break;
       need = next;
       ++j;
     }
     if (j == i)
       return fail(PM_EWORKSPACE, "workspace of %zu bytes cannot hold a %dx%d matrix (needs %zu)", ws_bytes,
-                  items[i].plan.rows, items[i].plan.cols, table_bytes(1) + items[i].plan.ws);
+                  items[i].plan.rows, items[i].plan.cols, table_bytes(1, gemm_launches(hp)) + items[i].plan.ws);
     const int rc = run_group(items.data() + i, (int)(j - i), group++, hp, mode, lr_dev, lr_host,
                              (char*)workspace, stream);
     if (rc) return rc;
@@ -333,7 +364,7 @@ size_t plan_workspace(const std::vector<Plan>& plans, const pm_hparams* hp) {
   }
   const uint64_t limit = hp->workspace_limit ? hp->workspace_limit : kDefaultWorkspaceLimit;
   const size_t body = std::min<size_t>(total, std::max<size_t>(limit, largest));
-  return table_bytes((int)plans.size()) + body;
+  return table_bytes((int)plans.size(), gemm_launches(hp)) + body;
 }
 
 int collect_step(const pm_matrix* mats, int n, std::vector<Item>& items) {
@@ -503,7 +534,7 @@ int pm_timing_read(pm_launch_time* out, int max) {
   return n;
 }
 
-size_t pm_gram_workspace_bytes(void) { return table_bytes(1); }
+size_t pm_gram_workspace_bytes(void) { return table_bytes(1, 1); }
 
 int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspace, size_t workspace_bytes,
             void* stream) {
@@ -512,9 +543,9 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   if (rc) return rc;
   if (!x || !out || !workspace) return fail(PM_EINVAL, "NULL pointer");
   if (rows % kTile || cols % kTile) return fail(PM_EINVAL, "pm_gram needs rows and cols that are multiples of 256");
-  if (workspace_bytes < table_bytes(1)) return fail(PM_EWORKSPACE, "workspace too small");
+  if (workspace_bytes < table_bytes(1, 1)) return fail(PM_EWORKSPACE, "workspace too small");
   if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
-  std::vector<char> host(table_bytes(1), 0);
+  std::vector<char> host(table_bytes(1, 1), 0);
   MatDesc* d = (MatDesc*)host.data();
   d->X[0] = (uint16_t*)x;
   d->A = (uint16_t*)out;
@@ -523,6 +554,7 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   d->rows = (int32_t)rows;
   d->cols = (int32_t)cols;
   int32_t* sym = (int32_t*)(host.data() + align_up(sizeof(MatDesc)) + align_up(8));
+  const size_t queues_off = align_up(sizeof(MatDesc)) + 3 * align_up(8);  // one launch's counters, zeros
   const int32_t nt = (int32_t)(rows / kTile);
   sym[0] = 0;
   sym[1] = nt * (nt + 1) / 2;
@@ -532,11 +564,13 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   GemmArgs ga{};
   ga.descs = (const MatDesc*)workspace;
   ga.prefix = (const int32_t*)((char*)workspace + ((char*)sym - host.data()));
+  ga.queues = (int32_t*)((char*)workspace + queues_off);
+  ga.total = sym[1];
   ga.n = 1;
   ga.stage = ST_GRAM;
   ga.cur = 0;
   ga.first = 0;
-  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym[1]), dim3(kGemmThreads), 0, s, ga);
+  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PM_OK : hip_fail(e, "gram launch");
 }

@@ -66,6 +66,8 @@ struct ProArgs {
 struct GemmArgs {
   const MatDesc* descs;
   const int32_t* prefix;  // n+1 prefix sums of this stage's tile counts
+  int32_t* queues;        // kXcds tile counters of this launch, zero at launch
+  int32_t total;          // tiles of this launch (prefix[n])
   int32_t n;
   int32_t stage;
   int32_t cur;            // which X/XT ping-pong buffer holds the current X
@@ -95,7 +97,8 @@ __device__ __forceinline__ void store_elem(void* p, int32_t dt, int64_t i, float
 }
 
 // Locate the matrix owning global work item t: prefix[lo] <= t < prefix[lo+1].
-__device__ __forceinline__ int find_matrix(const int32_t* __restrict__ prefix, int n, int t) {
+template <class P>
+__device__ __forceinline__ int find_matrix(P prefix, int n, int t) {
   int lo = 0, hi = n;
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;

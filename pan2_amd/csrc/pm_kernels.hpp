@@ -328,13 +328,21 @@ __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine&
   }
 }
 
-// Full K loop of one tile. K must be a multiple of 256 (padded extents), so
-// the unit count KT = K / 64 is a multiple of 4.
-__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, int ldl,
-                                              const uint16_t* __restrict__ Rp, int ldr, int K, const Ring& ring,
-                                              f32x4 (&acc)[kMi][kNi]) {
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar LDS bases
+// Lane index rebuilt from the exec mask inside an asm block with no inputs,
+// so neither it nor the per-lane offsets derived from it can be hoisted out of
+// the persistent tile loop (where they would stay live through the K loop);
+// the wave index lives in an SGPR.
+__device__ __forceinline__ int lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Operand panels and per-lane addressing of one tile.
+__device__ __forceinline__ Engine make_engine(const uint16_t* __restrict__ Lp, int ldl,
+                                              const uint16_t* __restrict__ Rp, int ldr, int w) {
+  const int lane = lane_id();
   Engine e;
   e.rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
   e.rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
@@ -355,15 +363,14 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
   for (int s = 0; s < 2; ++s) e.frag[s] = r16 * 128 + (((4 * s + g) ^ ((r16 >> 1) & 7)) << 4);
   e.aofs = (w >> 2) * kWaveRows * 128;
   e.bofs = (w & 3) * kWaveCols * 128;
+  return e;
+}
 
-#pragma unroll
-  for (int i = 0; i < kMi; ++i)
-#pragma unroll
-    for (int j = 0; j < kNi; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  bf16x8 bf[2][kNi];
-  bf16x8 af[8];
-
-  // Unit 0 whole, then what a unit -1 would issue at its positions 12..15.
+// Copies of unit 0 and the first 6 of unit 1 (what a unit -1 would issue at
+// its positions 12..15); unit 0's positions 0, 1 issue the other two. May be
+// issued while the previous tile's epilogue runs: it touches only the LDS
+// ring, which the caller has certified free with a barrier.
+__device__ __forceinline__ void gemm_prefetch(const Engine& e, const Ring& ring) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) dma_b(e, ring.b[0], 0, i);
 #pragma unroll
@@ -374,7 +381,23 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ Lp, i
   dma_a(e, ring.a[1], 1, 0);
   dma_b(e, ring.b[1], 1, 3);
   dma_a(e, ring.a[1], 1, 1);
-  wait_vmcnt<6>();  // unit 0 landed
+}
+
+// Full K loop of one tile whose first copies gemm_prefetch issued. K must be a
+// multiple of 256 (padded extents), so the unit count KT = K / 64 is a
+// multiple of 4. Every wave waits for all its memory operations first (the
+// prefetch, and the previous tile's epilogue stores, which vmcnt also counts),
+// so the in-loop counts see only this tile's copies.
+__device__ __forceinline__ void gemm_run(const Engine& e, int K, const Ring& ring, f32x4 (&acc)[kMi][kNi]) {
+#pragma unroll
+  for (int i = 0; i < kMi; ++i)
+#pragma unroll
+    for (int j = 0; j < kNi; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  bf16x8 bf[2][kNi];
+  bf16x8 af[8];
+
+  wait_vmcnt<0>();
+  wait_lgkmcnt<0>();  // also publishes LDS writes made before this barrier
   block_barrier();
 #pragma unroll
   for (int i = 0; i < kNi; ++i) bf[0][i] = *(const bf16x8*)(ring.b[0] + e.bofs + i * 2048 + e.frag[0]);
@@ -428,16 +451,6 @@ __device__ __forceinline__ void for_each_quad(const f32x4 (&acc)[kMi][kNi], int 
     }
 }
 
-// Loads, for every quad of this lane, the 4 consecutive elements T[q][p0..p0+3]
-// of a row-major matrix T (ld elements): 8-byte loads, all issued before use.
-__device__ __forceinline__ void load_quads(u16x4 (&v)[kQuads], const uint16_t* __restrict__ T, int64_t ld,
-                                           int pbase, int qbase) {
-#pragma unroll
-  for (int mi = 0; mi < kMi; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < kNi; ++ni)
-      v[mi * kNi + ni] = *(const u16x4*)(T + (int64_t)(qbase + ni * 16) * ld + pbase + mi * 16);
-}
 
 // Operands and tile of one work item of stage STAGE.
 struct TileJob {
@@ -447,8 +460,8 @@ struct TileJob {
   int ti, tj;
 };
 
-template <int STAGE>
-__device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur) {
+template <int STAGE, class D>
+__device__ __forceinline__ TileJob decode_tile(const D& d, int lt, int cur) {
   TileJob j;
   int P, Q;
   bool sym = false;
@@ -476,6 +489,99 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
   return j;
 }
 
+// 4x4 transpose of bf16 values across each group of 4 lanes. Lane l holds
+// rows 0..3 of column l%4 of a 4x4 block (its accumulator quad); afterwards it
+// holds columns 0..3 of row l%4, i.e. 4 consecutive elements of one row of a
+// row-major output, stored with one 8-byte store instead of four 2-byte ones.
+// Dwords are exchanged with lane l^2 (DPP quad_perm [2,3,0,1]), then 16-bit
+// halves with lane l^1 (quad_perm [1,0,3,2]) and reassembled by v_perm_b32.
+// All 64 lanes must be active.
+__device__ __forceinline__ u16x4 quad_transpose(u16x4 v, int lane) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 d = __builtin_bit_cast(u32x2, v);  // d.x = rows 0,1; d.y = rows 2,3
+  const bool low = (lane & 2) == 0;
+  const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)(low ? d.y : d.x), 0x4E, 0xF, 0xF, false);
+  const uint32_t a0 = low ? d.x : recv;  // rows 2(l/2%2)+{0,1} of column l%2
+  const uint32_t a1 = low ? recv : d.y;  // the same rows of column l%2 + 2
+  const uint32_t p0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)a0, 0xB1, 0xF, 0xF, false);
+  const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)a1, 0xB1, 0xF, 0xF, false);
+  const uint32_t sel = (lane & 1) ? 0x03020706u : 0x05040100u;  // odd: high halves, even: low halves
+  const u32x2 o = {__builtin_amdgcn_perm(p0, a0, sel), __builtin_amdgcn_perm(p1, a1, sel)};
+  return __builtin_bit_cast(u16x4, o);
+}
+
+// Pairs the quads a = (mi, ni) and b = (mi, ni+1) of the transposed output
+// Cᵀ[q][p]: lanes of 16-lane rows 0 and 2 end up with 8 consecutive p of a's
+// column, rows 1 and 3 with 8 consecutive p of b's column (v_permlane16_swap
+// exchanges odd rows of its first operand with even rows of its second), so
+// every lane stores 16 contiguous bytes at Cᵀ[q + 16(g&1)][p0 - 4(g&1)],
+// g = lane/16. All 64 lanes must be active.
+__device__ __forceinline__ u32x4 pair_rows(u16x4 a, u16x4 b) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 x = __builtin_bit_cast(u32x2, a), y = __builtin_bit_cast(u32x2, b);
+  const auto s0 = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
+  const auto s1 = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
+  return (u32x4){s0[0], s1[0], s0[1], s1[1]};
+}
+
+// Loads, for every quad of this lane, the 4 consecutive elements T[q][p0..p0+3]
+// of a row-major matrix T (ld elements). Quads (mi, ni) and (mi, ni+1) travel
+// together as one 16-byte load in the paired layout of pair_rows, which
+// v_permlane16_swap (its own inverse) turns back into the two quads. All
+// loads are issued before any swap.
+__device__ __forceinline__ void load_quads(u16x4 (&v)[kQuads], const uint16_t* __restrict__ T, int64_t ld,
+                                           int pbase, int qbase, int lane) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const int g1 = (lane >> 4) & 1;
+  u32x4 w[kQuads / 2];
+#pragma unroll
+  for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < kNi; ni += 2)
+      w[(mi * kNi + ni) / 2] =
+          *(const u32x4*)(T + (int64_t)(qbase + (ni + g1) * 16) * ld + pbase + mi * 16 - 4 * g1);
+#pragma unroll
+  for (int k = 0; k < kQuads / 2; ++k) {
+    const auto s0 = __builtin_amdgcn_permlane16_swap(w[k].x, w[k].z, false, false);
+    const auto s1 = __builtin_amdgcn_permlane16_swap(w[k].y, w[k].w, false, false);
+    v[2 * k] = __builtin_bit_cast(u16x4, (u32x2){s0[0], s1[0]});
+    v[2 * k + 1] = __builtin_bit_cast(u16x4, (u32x2){s0[1], s1[1]});
+  }
+}
+
+// Register vector of 4 param elements of the FINAL epilogue.
+template <bool F32> struct PickVec { typedef u16x4 type; typedef uint16_t elem; };
+template <> struct PickVec<true> { typedef f32x4 type; typedef float elem; };
+
+// Tile counters: the tiles of a launch form kXcds queues, queue x holding the
+// virtual indices v = x + kXcds*k in order, each mapped to a tile by
+// xcd_remap (a permutation of [0, total)). A block serves the queue of the XCD
+// it runs on, so an XCD walks runs of kXcdChunk neighbouring tiles whose
+// panels its L2 shares, and takes tiles from the other queues once its own is
+// empty, so XCDs that run slower finish no later than the rest. Returns -1
+// when every queue is empty. Called by one lane; *home (in LDS, so no register
+// stays live across the K loop) is the queue to try first and follows the
+// queue that last had work.
+__device__ __forceinline__ int grab_tile(int32_t* queues, int total, int* home) {
+  const int h = *home;
+#pragma unroll 1
+  for (int i = 0; i < kXcds; ++i) {
+    const int y = (h + i) & (kXcds - 1);
+    const int len = total > y ? (total - y + kXcds - 1) / kXcds : 0;
+    if (len == 0) continue;
+    const int k = __hip_atomic_fetch_add(queues + y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k < len) {
+      *home = y;
+      return xcd_remap(y + kXcds * k, total);
+    }
+  }
+  return -1;
+}
+
+__device__ __forceinline__ int xcc_id() {
+  return (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (kXcds - 1));  // HW_REG_XCC_ID[3:0]
+}
+
 // One Newton–Schulz stage over every matrix of the group.
 //   GRAM   A = s·X Xᵀ            (s = 1/‖X‖² at iteration 0, folding
 //                                 X.div_(norm) of torch/optim/_muon.py:59)
@@ -489,26 +595,12 @@ __device__ __forceinline__ TileJob decode_tile(const MatDesc& d, int lt, int cur
 // to bf16 where torch rounds it.
 // PDT is the param dtype of the FINAL epilogue (one instantiation per dtype
 // keeps the epilogue's registers within budget); other stages ignore it.
-template <int STAGE, int PDT = DT_BF16>
-__global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
+template <int STAGE, int PDT, class D>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, const TileJob& job,
+                                              const f32x4 (&acc)[kMi][kNi], int wave) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(1024))) char lds_a0[kOpBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_a1[kOpBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_b0[kOpBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_b1[kOpBytes];
-  const Ring ring{{lds_a0, lds_a1}, {lds_b0, lds_b1}};
-
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int m = find_matrix(args.prefix, args.n, t);
-  const MatDesc& d = args.descs[m];
   const int cur = args.cur;
-  const TileJob job = decode_tile<STAGE>(d, t - args.prefix[m], cur);
-
-  f32x4 acc[kMi][kNi];
-  gemm_mainloop(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl, job.R + (int64_t)job.tj * kTile * job.ldr,
-                job.ldr, job.K, ring, acc);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = lane_id();
   const int pbase = job.ti * kTile + (wave >> 2) * kWaveRows + 4 * (lane >> 4);
   const int qbase = job.tj * kTile + (wave & 3) * kWaveCols + (lane & 15);
 
@@ -523,17 +615,27 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     const float cb = args.b, cc = args.c;
     const bool mirror = job.ti != job.tj;
     u16x4 av[kQuads];
-    if (STAGE == ST_POLY) load_quads(av, d.A, ldc, pbase, qbase);
-    for_each_quad(acc, pbase, qbase, [&](int i, int p0, int q, const float (&x)[4]) {
-      u16x4 o;
+    if (STAGE == ST_POLY) load_quads(av, d.A, ldc, pbase, qbase, lane);
+    const int g1 = (lane >> 4) & 1;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float v = (STAGE == ST_GRAM) ? x[r] * s : cc * x[r] + cb * bf2f(av[i][r]);
-        o[r] = f2bf(v);
-        C[(int64_t)(p0 + r) * ldc + q] = o[r];
+    for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < kNi; ni += 2) {
+        const int p0 = pbase + mi * 16;
+        u16x4 o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int i = mi * kNi + ni + h, q = qbase + (ni + h) * 16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = acc[mi][ni + h][r];
+            o[h][r] = f2bf((STAGE == ST_GRAM) ? x * s : cc * x + cb * bf2f(av[i][r]));
+          }
+          *(u16x4*)(C + (int64_t)(p0 + (lane & 3)) * ldc + (q & ~3)) = quad_transpose(o[h], lane);
+        }
+        if (mirror)
+          *(u32x4*)(C + (int64_t)(qbase + (ni + g1) * 16) * ldc + p0 - 4 * g1) = pair_rows(o[0], o[1]);
       }
-      if (mirror) *(u16x4*)(C + (int64_t)q * ldc + p0) = o;
-    });
     return;
   }
 
@@ -544,16 +646,23 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     uint16_t* XTn = d.XT[cur ^ 1];
     const int64_t ldx = d.Np, ldxt = d.Mp;
     u16x4 xv[kQuads];
-    load_quads(xv, d.XT[cur], ldxt, pbase, qbase);  // X[p][q] = Xᵀ[q][p]
-    for_each_quad(acc, pbase, qbase, [&](int i, int p0, int q, const float (&x)[4]) {
-      u16x4 o;
+    load_quads(xv, d.XT[cur], ldxt, pbase, qbase, lane);  // X[p][q] = Xᵀ[q][p]
+    const int g1 = (lane >> 4) & 1;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        o[r] = f2bf((ca * bf2f(xv[i][r]) + x[r]) * s);
-        Xn[(int64_t)(p0 + r) * ldx + q] = o[r];
+    for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < kNi; ni += 2) {
+        const int p0 = pbase + mi * 16;
+        u16x4 o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int i = mi * kNi + ni + h, q = qbase + (ni + h) * 16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[h][r] = f2bf((ca * bf2f(xv[i][r]) + acc[mi][ni + h][r]) * s);
+          *(u16x4*)(Xn + (int64_t)(p0 + (lane & 3)) * ldx + (q & ~3)) = quad_transpose(o[h], lane);
+        }
+        *(u32x4*)(XTn + (int64_t)(qbase + (ni + g1) * 16) * ldxt + p0 - 4 * g1) = pair_rows(o[0], o[1]);
       }
-      *(u16x4*)(XTn + (int64_t)q * ldxt + p0) = o;
-    });
     return;
   }
 
@@ -561,8 +670,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   // param row q, columns p0..p0+3, and its a·X term is T[q][p0..p0+3] with T
   // the orientation of X whose rows are param rows. Loads and stores are
   // 8-byte (bf16) or 16-byte (fp32) vectors where the param's row stride and
-  // base allow, else per element. Bands of 8 quads are software-pipelined:
-  // band mi+1's loads are issued before band mi is combined and stored.
+  // base allow, else per element.
   const uint16_t* T = d.trans ? d.XT[cur] : d.X[cur];
   const int64_t ldt = d.trans ? d.Mp : d.Np;
   const int prow = d.rows, pcol = d.cols;
@@ -582,79 +690,141 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   constexpr bool f32p = PDT == DT_F32;  // MODE_NS launches the bf16 instantiation
   const int vec_align = f32p ? 16 : 8;
   const bool vec = (ldp % 4 == 0) && ((uintptr_t)d.param % vec_align == 0);
-  constexpr int kBand = kNi;  // quads of one 16-row band: kNi param rows x 4 columns
-  u16x4 xv[2][kBand];
-  float pv[2][kBand][4];
-  auto load_band = [&](int mi, u16x4 (&x)[kBand], float (&pp)[kBand][4]) {
+  // Bands of kNi quads (16 tile rows = kNi param rows x 4 columns each) are
+  // handled kBatch at a time: every load of a batch is issued before any of
+  // its results is combined, so a tile pays 8 / kBatch memory round trips.
+  // bf16 params travel as raw bf16 (2 registers a quad), fp32 as fp32 (4).
+  constexpr int kBatch = f32p ? 2 : 4;
+  typedef typename PickVec<f32p>::type PV;
 #pragma unroll
-    for (int j = 0; j < kBand; ++j) {
-      const int c0 = pbase + mi * 16, r = qbase + j * 16;  // param row r, columns c0..c0+3
-      x[j] = *(const u16x4*)(T + (int64_t)r * ldt + c0);
-      if (!step) continue;
-      const bool full = vec && r < prow && c0 + 3 < pcol;
-      if (f32p) {
-        const float* src = (const float*)d.param + (int64_t)r * ldp + c0;
-        if (full) {
-          const f32x4 v = *(const f32x4*)src;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pp[j][e] = v[e];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pp[j][e] = (r < prow && c0 + e < pcol) ? src[e] : 0.0f;
-        }
-      } else {
-        const uint16_t* src = (const uint16_t*)d.param + (int64_t)r * ldp + c0;
-        if (full) {
-          const u16x4 v = *(const u16x4*)src;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pp[j][e] = bf2f(v[e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pp[j][e] = (r < prow && c0 + e < pcol) ? bf2f(src[e]) : 0.0f;
-        }
-      }
-    }
-  };
-  auto store_band = [&](int mi, const u16x4 (&x)[kBand], const float (&pp)[kBand][4]) {
-#pragma unroll
-    for (int j = 0; j < kBand; ++j) {
-      const int c0 = pbase + mi * 16, r = qbase + j * 16;
-      if (r >= prow) continue;
-      float o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float on = bf2f(f2bf((ca * bf2f(x[j][e]) + acc[mi][j][e]) * s));  // bf16 orthogonalised update
-        o[e] = step ? pp[j][e] * wdf + on * neg : on;
-      }
-      const bool full = vec && c0 + 3 < pcol;
-      if (f32p) {
-        float* dst = (float*)d.param + (int64_t)r * ldp + c0;
-        if (full) {
-          *(f32x4*)dst = (f32x4){o[0], o[1], o[2], o[3]};
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (c0 + e < pcol) dst[e] = o[e];
-        }
-      } else {
-        uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
-        if (full) {
-          *(u16x4*)dst = (u16x4){f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (c0 + e < pcol) dst[e] = f2bf(o[e]);
-        }
-      }
-    }
-  };
-  load_band(0, xv[0], pv[0]);
-#pragma unroll
-  for (int mi = 0; mi < kMi; ++mi) {
-    // one band per scheduling region, so bands are not interleaved (register pressure)
+  for (int b0 = 0; b0 < kMi; b0 += kBatch) {
     __builtin_amdgcn_sched_barrier(0);
-    if (mi + 1 < kMi) load_band(mi + 1, xv[(mi + 1) & 1], pv[(mi + 1) & 1]);
-    store_band(mi, xv[mi & 1], pv[mi & 1]);
+    u16x4 xv[kBatch][kNi];
+    PV pv[kBatch][kNi];
+#pragma unroll
+    for (int bi = 0; bi < kBatch; ++bi)
+#pragma unroll
+      for (int j = 0; j < kNi; ++j) {
+        const int c0 = pbase + (b0 + bi) * 16, r = qbase + j * 16;  // param row r, columns c0..c0+3
+        xv[bi][j] = *(const u16x4*)(T + (int64_t)r * ldt + c0);
+        if (!step) continue;
+        const bool in_row = r < prow;
+        typedef typename PickVec<f32p>::elem E;
+        const E* src = (const E*)d.param + (int64_t)r * ldp + c0;
+        if (vec && in_row && c0 + 3 < pcol) {
+          pv[bi][j] = *(const PV*)src;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pv[bi][j][e] = (in_row && c0 + e < pcol) ? src[e] : (E)0;
+        }
+      }
+#pragma unroll
+    for (int bi = 0; bi < kBatch; ++bi)
+#pragma unroll
+      for (int j = 0; j < kNi; ++j) {
+        const int mi = b0 + bi;
+        const int c0 = pbase + mi * 16, r = qbase + j * 16;
+        if (r >= prow) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float on = bf2f(f2bf((ca * bf2f(xv[bi][j][e]) + acc[mi][j][e]) * s));  // bf16 orthogonalised update
+          const float pe = f32p ? (float)pv[bi][j][e] : bf2f((uint16_t)pv[bi][j][e]);
+          o[e] = step ? pe * wdf + on * neg : on;
+        }
+        const bool full = vec && c0 + 3 < pcol;
+        if (f32p) {
+          float* dst = (float*)d.param + (int64_t)r * ldp + c0;
+          if (full) {
+            *(f32x4*)dst = (f32x4){o[0], o[1], o[2], o[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (c0 + e < pcol) dst[e] = o[e];
+          }
+        } else {
+          uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
+          if (full) {
+            *(u16x4*)dst = (u16x4){f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (c0 + e < pcol) dst[e] = f2bf(o[e]);
+          }
+        }
+      }
+  }
+}
+
+// Persistent GEMM launch: one block per CU (grid = min(tiles, CUs)), each
+// taking tiles from the queues until they are empty. The next tile's first
+// copies are issued before the current tile's epilogue, so its pipeline
+// fills while the epilogue's loads and stores run.
+// The next tile index travels through s_tile: lane 0 takes it from the queues
+// during the previous epilogue and writes slot slot^1, which the waves read
+// after the barrier that ends the following tile's K loop; a slot is
+// rewritten only after every wave has passed the barrier that follows its read.
+template <int STAGE, int PDT = DT_BF16>
+__global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
+  __shared__ __attribute__((aligned(1024))) char lds_a0[kOpBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_a1[kOpBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b0[kOpBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b1[kOpBytes];
+  __shared__ int s_tile[2];
+  __shared__ int s_home;
+  const Ring ring{{lds_a0, lds_a1}, {lds_b0, lds_b1}};
+
+  // The descriptor table does not change during the launch: reading it
+  // through the constant address space keeps its loads scalar (SGPRs) even
+  // after the epilogue's stores.
+  typedef const __attribute__((address_space(4))) MatDesc* DescPtr;
+  typedef const __attribute__((address_space(4))) int32_t* PrefixPtr;
+  const DescPtr descs = (DescPtr)args.descs;
+  const PrefixPtr prefix = (PrefixPtr)args.prefix;
+  const int total = args.total;
+  const int wave = wave_id();
+  if (threadIdx.x == 0) {
+    s_home = xcc_id();
+    const int t0 = grab_tile(args.queues, total, &s_home);
+    s_tile[0] = t0;
+    s_tile[1] = t0 >= 0 ? grab_tile(args.queues, total, &s_home) : -1;
+  }
+  __syncthreads();
+  int t = __builtin_amdgcn_readfirstlane(s_tile[0]);
+  if (t < 0) return;
+  int slot = 1;
+
+  int m = find_matrix(prefix, args.n, t);
+  TileJob job = decode_tile<STAGE>(descs[m], t - prefix[m], args.cur);
+  gemm_prefetch(make_engine(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl,
+                            job.R + (int64_t)job.tj * kTile * job.ldr, job.ldr, wave),
+                ring);
+  for (;;) {
+    f32x4 acc[kMi][kNi];
+    gemm_run(make_engine(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl,
+                         job.R + (int64_t)job.tj * kTile * job.ldr, job.ldr, wave),
+             job.K, ring, acc);
+    block_barrier();  // every wave is past its last LDS read of this tile
+    const int tn = __builtin_amdgcn_readfirstlane(s_tile[slot]);
+    int mn = 0;
+    TileJob jn{};
+    if (tn >= 0) {
+      mn = find_matrix(prefix, args.n, tn);
+      jn = decode_tile<STAGE>(descs[mn], tn - prefix[mn], args.cur);
+      gemm_prefetch(make_engine(jn.L + (int64_t)jn.ti * kTile * jn.ldl, jn.ldl,
+                                jn.R + (int64_t)jn.tj * kTile * jn.ldr, jn.ldr, wave),
+                    ring);
+    }
+    const bool leader = wave == 0 && lane_id() == 0;
+    int after = -1;
+    if (leader && tn >= 0) after = grab_tile(args.queues, total, &s_home);
+    gemm_epilogue<STAGE, PDT>(args, descs[m], job, acc, wave);
+    if (leader) s_tile[slot ^ 1] = after;
+    if (tn < 0) break;
+    t = tn;
+    m = mn;
+    job = jn;
+    slot ^= 1;
   }
 }
 

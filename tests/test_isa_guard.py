@@ -74,3 +74,12 @@ def test_loads_do_not_overwrite_queued_mfma_sources(gemm_kernels):
                     t.startswith("buffer_load") and " lds" not in t):
                 dst = _regs(t.split(None, 1)[1].split(",")[0].strip())
                 assert not any(dst & src for src in recent), f"{name}: {t}"
+
+
+def test_no_scalar_memory_writes(gemm_kernels):
+    """Every store and atomic goes through the vector memory path (the tile
+    queues' counters included)."""
+    bad = re.compile(r"^\s*(s_store|s_buffer_store|s_atomic|s_buffer_atomic|s_scratch_store|s_dcache_wb)")
+    for name, lines in gemm_kernels.items():
+        hits = [ln.strip() for ln in lines if bad.match(ln)]
+        assert not hits, f"{name}: {hits[:2]}"
