@@ -46,6 +46,26 @@ def dense_flops(shape, steps=5):
     return steps * (4 * m * m * n + 2 * m ** 3)
 
 
+def gram_form_flops(shape, steps=5):
+    """Algorithmic FLOPs of PAN 2's gram form (pan/optim/patch_muon.py:275-334):
+    two symmetric grams, two applications Q X, and the symmetric M^3 products
+    (Z every iteration, Q from the second of a segment, RZ and R unless the
+    next iteration resets or ends)."""
+    m, n = min(shape), max(shape)
+    reset = 2 if steps > 2 else -1
+    sym, segment_start = 0, True
+    for i in range(steps):
+        if i == reset:
+            segment_start = True
+        sym += 1 if segment_start else 2
+        segment_start = False
+        if i + 1 < steps and i + 1 != reset:
+            sym += 2
+    grams = 2 if reset >= 0 else 1
+    applies = 2 if reset >= 0 else 1
+    return grams * m * (m + 1) * n + sym * m * m * (m + 1) + applies * 2 * m * m * n
+
+
 def build_state(shapes, config, device, seed=1234):
     """Params/grads/momentum resident on the device (BASELINE dtypes)."""
     import torch
@@ -131,12 +151,53 @@ def traffic_summary(args) -> int:
     return 0
 
 
+def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
+    """Fixed NS (or hipBLASLt bmm) workload for rocprofv3 counter runs; prints one line per stage."""
+    import torch
+
+    from pan2_amd import _lib
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    if which == "bmm":
+        a = torch.randn(batch, size, size, device=dev, dtype=torch.bfloat16, generator=gen)
+        b = torch.randn(batch, size, size, device=dev, dtype=torch.bfloat16, generator=gen)
+        torch.bmm(a, b)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            torch.bmm(a, b)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        print(f"probe bmm {batch}x{size}^3: {dt * 1e3:.2f} ms, {2 * batch * size ** 3 / dt / 1e12:.1f} TFLOP/s")
+        return 0
+    xs = [torch.randn(size, size, device=dev, dtype=torch.bfloat16, generator=gen) for _ in range(batch)]
+    outs = [torch.empty_like(x) for x in xs]
+    _lib.newton_schulz_into(list(zip(xs, outs)))
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    _lib.timing_read()
+    for _ in range(reps):
+        _lib.newton_schulz_into(list(zip(xs, outs)))
+    recs = _lib.timing_read()
+    _lib.timing_enable(False)
+    for kind in ("gram", "poly", "update", "final"):
+        rs = [r for r in recs if r["kind"] == kind]
+        ms = sum(r["ms"] for r in rs)
+        print(f"probe ns {batch}x{size}^2 {kind}: {ms / reps:.2f} ms per call, "
+              f"{sum(r['flops'] for r in rs) / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", type=int, default=5, choices=sorted(CONFIGS))
+    ap.add_argument("--ns-form", default="standard", choices=("standard", "gram"),
+                    help="standard: torch's quintic (the BASELINE metric); gram: PAN 2's production gram form, "
+                         "reported with its own (smaller) executed FLOP count")
     ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workspace-gib", type=float, default=0.0, help="libpanmuon workspace cap (0 = default)")
@@ -147,9 +208,15 @@ def main() -> int:
                          "per GEMM launch (needs --fetch-csv, --write-csv, --copy-mib)")
     ap.add_argument("--fetch-csv")
     ap.add_argument("--write-csv")
+    ap.add_argument("--probe", choices=("ns", "bmm"),
+                    help="counter probe instead of the Muon step: 'ns' runs Newton-Schulz alone on 16 x 5120^2 "
+                         "bf16 matrices through pm_newton_schulz, 'bmm' the same 16 x 5120^3 products through "
+                         "torch.bmm (hipBLASLt) for comparison")
     args = ap.parse_args()
     if args.traffic_summary:
         return traffic_summary(args)
+    if args.probe:
+        return probe(args.probe)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU sharding is a design, not code", file=sys.stderr)
@@ -170,7 +237,7 @@ def main() -> int:
     print(f"bench: config {args.config} ({name}), {len(shapes)} matrices, building state", file=sys.stderr, flush=True)
     t0 = time.time()
     params, moms = build_state(shapes, args.config, device)
-    patch_muon()
+    patch_muon(ns_form=args.ns_form)
     if args.workspace_gib:
         pm.WORKSPACE_LIMIT = int(args.workspace_gib * (1 << 30))
     lr = torch.tensor(0.02, dtype=torch.float32, device=device)
@@ -208,14 +275,16 @@ def main() -> int:
 
     f_ns = sum(ns_flops(s) for s in shapes)
     f_dense = sum(dense_flops(s) for s in shapes)
-    value = f_ns / (ms_per_step * 1e-3) / 1e12
+    # the gram form does less work than the quintic: its rate is its own executed FLOPs over time
+    f_run = f_ns if args.ns_form == "standard" else sum(gram_form_flops(s) for s in shapes)
+    value = f_run / (ms_per_step * 1e-3) / 1e12
 
     gemm = [r for r in recs if r["kind"] in ("gram", "poly", "update", "final")]
     gemm_ms = sum(r["ms"] for r in gemm)
     gemm_flops = sum(r["flops"] for r in gemm)
     achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
     stages = {}
-    for kind in ("prologue", "norm", "gram", "poly", "update", "final"):
+    for kind in ("prologue", "norm", "gram", "poly", "qinit", "update", "final"):
         rs = [r for r in recs if r["kind"] == kind]
         if not rs:
             continue
@@ -271,8 +340,10 @@ def main() -> int:
             "grad_dtype": "fp32" if args.config == 1 else "bf16",
             "momentum_dtype": "fp32",
             "ns_steps": 5,
+            "ns_form": args.ns_form,
             "f_ns": f_ns,
             "f_dense": f_dense,
+            **({"f_gram_form": f_run} if args.ns_form == "gram" else {}),
         },
         "pct_peak_step": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "roofline": {

@@ -18,11 +18,18 @@
  *   - Matrices are row-major with unit column stride and a row stride ("ld")
  *     in elements.
  *
- * Newton–Schulz is the standard quintic of torch.optim._muon
- * (_zeropower_via_newtonschulz, torch/optim/_muon.py:31-70): per iteration
- * A = X Xᵀ, B = b A + c A², X <- a X + B X, with X oriented so that its short
- * side is contracted. Operands are bf16, accumulation fp32, and every GEMM
- * output is rounded to bf16 exactly where torch rounds it.
+ * Newton–Schulz comes in two organisations (pm_hparams.ns_form):
+ *   PM_NS_STANDARD: the quintic of torch.optim._muon
+ *     (_zeropower_via_newtonschulz, torch/optim/_muon.py:31-70): per
+ *     iteration A = X Xᵀ, B = b A + c A², X <- a X + B X.
+ *   PM_NS_GRAM: PAN 2's production form (_gram_newtonschulz_local,
+ *     pan/optim/patch_muon.py:275-334): the iteration runs on the gram
+ *     R = X Xᵀ and accumulates the polynomial Q, so only two grams and two
+ *     applications X <- Q X touch the full matrix (X is re-grammed at
+ *     iteration 2). Equal to the standard form in exact arithmetic.
+ * X is oriented so that its short side is contracted. Operands are bf16,
+ * accumulation fp32, and every GEMM output is rounded to bf16 where the
+ * reference rounds it.
  */
 #ifndef PANMUON_H
 #define PANMUON_H
@@ -34,12 +41,18 @@
 extern "C" {
 #endif
 
-#define PM_ABI_VERSION 1
+#define PM_ABI_VERSION 2
 
 /* Element types accepted for params, grads, momentum buffers and updates. */
 enum pm_dtype {
   PM_DTYPE_F32 = 0,
   PM_DTYPE_BF16 = 1
+};
+
+/* pm_hparams.ns_form */
+enum pm_ns_form {
+  PM_NS_STANDARD = 0,
+  PM_NS_GRAM = 1
 };
 
 enum pm_status {
@@ -94,6 +107,8 @@ typedef struct pm_ns_matrix {
  * ns_steps, eps, weight_decay.
  *   coeffs: NULL to use (a, b, c) for every iteration, or a host array of
  *           ns_steps triples (a, b, c) — one per iteration.
+ *   ns_form: PM_NS_STANDARD (torch's quintic) or PM_NS_GRAM (PAN 2's gram
+ *           form, pan/optim/patch_muon.py:275-334).
  *   workspace_limit: upper bound in bytes on the workspace pm_workspace_bytes
  *           asks for (0 = library default); matrices are then processed in
  *           groups that fit.
@@ -107,6 +122,7 @@ typedef struct pm_hparams {
   float a;
   float b;
   float c;
+  int32_t ns_form;
   const float* coeffs;
   uint64_t workspace_limit;
 } pm_hparams;
@@ -183,6 +199,21 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out,
             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Symmetric product out = alpha * L Rᵀ + beta * D on m x m bf16 matrices
+ * (fp32 accumulate, bf16 out). Only the upper triangle is computed (the
+ * 256 x 256 tiles on and above the diagonal) and it is mirrored, so the
+ * result is exactly symmetric. Replaces quack gemm_symmetric_out(L, R, out=out, C=D, alpha,
+ * beta) and gemm_symmetric(L, R, C=D, beta=beta) as PAN 2's gram form calls
+ * them (pan/optim/patch_muon.py:320-331), where R and D are symmetric (so
+ * L Rᵀ = L R) and L, R commute. D may be NULL when beta == 0 (it is then not
+ * read). All matrices have ld == m; m must be a multiple of 256. out must not
+ * alias L, R or D.
+ */
+size_t pm_gemm_symmetric_workspace_bytes(void);
+int pm_gemm_symmetric(const void* left, const void* right, const void* addend, void* out, int64_t m,
+                      float alpha, float beta, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Opt-in launch timing (no counterpart in the reference, which has no
  * instrumentation; used by bench.py for live roofline figures). While enabled,
  * every launch of pm_muon_step / pm_newton_schulz records a HIP event on the
@@ -193,9 +224,11 @@ enum pm_kernel_kind {
   PM_K_PROLOGUE = 0,  /* momentum + bf16 X/Xᵀ + Σx² partials */
   PM_K_NORM = 1,      /* per-matrix 1/‖X‖ */
   PM_K_GRAM = 2,      /* A = X Xᵀ (symmetric) */
-  PM_K_POLY = 3,      /* B = b A + c A² (symmetric) */
-  PM_K_UPDATE = 4,    /* X <- a X + B X */
-  PM_K_FINAL = 5      /* last update fused with the parameter step */
+  PM_K_POLY = 3,      /* symmetric product: B = b A + c A² (standard form);
+                         Z, Q, RZ and R updates (gram form) */
+  PM_K_UPDATE = 4,    /* X <- a X + B X (gram form: X <- Q X at the reset) */
+  PM_K_FINAL = 5,     /* last update fused with the parameter step */
+  PM_K_QINIT = 6      /* gram form: Q = Z + a I */
 };
 
 typedef struct pm_launch_time {

@@ -188,11 +188,13 @@ def quintic_power(x, ns_coefficients=DEFAULT_COEFFS, ns_steps: int = DEFAULT_NS_
 def muon_step(param, grad, buf, *, lr: float, weight_decay: float, momentum: float = 0.95,
               nesterov: bool = True, ns_coefficients=DEFAULT_COEFFS, ns_steps: int = DEFAULT_NS_STEPS,
               eps: float = EPS, adjust_lr_fn=None, shape: Sequence[int] | None = None,
-              ns_precision: str = "fp32"):
-    """One Muon step of one matrix, pan/optim/patch_muon.py:149-171 with the
-    standard NS: returns (new_param, new_buf, O)."""
+              ns_precision: str = "fp32", ns_form: str = "standard"):
+    """One Muon step of one matrix, pan/optim/patch_muon.py:149-171, with the
+    standard NS (torch's quintic) or PAN 2's gram form (ns_form="gram",
+    pan/optim/patch_muon.py:275-334): returns (new_param, new_buf, O)."""
     nb, u = momentum_nesterov(buf, grad, momentum, nesterov)
-    O = ns_standard(u, ns_coefficients, ns_steps, eps, precision=ns_precision)
+    ns = {"standard": ns_standard, "gram": ns_gram}[ns_form]
+    O = ns(u, ns_coefficients, ns_steps, eps, precision=ns_precision)
     ratio = adjust_lr_ratio(adjust_lr_fn, shape if shape is not None else np.shape(param))
     if ns_precision != "fp64":
         O = round_bf16(O) if ns_precision == "bf16" else O.astype(np.float32)

@@ -13,10 +13,15 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpanmuon.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PM_DTYPE_F32 = 0
 PM_DTYPE_BF16 = 1
+
+# Newton–Schulz organisation (pm_hparams.ns_form)
+PM_NS_STANDARD = 0
+PM_NS_GRAM = 1
+NS_FORMS = {"standard": PM_NS_STANDARD, "gram": PM_NS_GRAM}
 
 PM_EINVAL = -1
 PM_EDTYPE = -2
@@ -36,11 +41,13 @@ EXPORTS = (
     "pm_step_param",
     "pm_gram_workspace_bytes",
     "pm_gram",
+    "pm_gemm_symmetric_workspace_bytes",
+    "pm_gemm_symmetric",
     "pm_timing_enable",
     "pm_timing_read",
 )
 
-KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final")
+KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit")
 
 
 class PmMatrix(ctypes.Structure):
@@ -84,6 +91,7 @@ class PmHparams(ctypes.Structure):
         ("a", ctypes.c_float),
         ("b", ctypes.c_float),
         ("c", ctypes.c_float),
+        ("ns_form", ctypes.c_int32),
         ("coeffs", ctypes.POINTER(ctypes.c_float)),
         ("workspace_limit", ctypes.c_uint64),
     ]
@@ -132,6 +140,8 @@ def load() -> ctypes.CDLL:
             "pm_step_param": (ctypes.c_int, [vp, i32, vp, i32, i64, vp, f64, f32, f64, vp]),
             "pm_gram_workspace_bytes": (sz, []),
             "pm_gram": (ctypes.c_int, [vp, i64, i64, vp, vp, sz, vp]),
+            "pm_gemm_symmetric_workspace_bytes": (sz, []),
+            "pm_gemm_symmetric": (ctypes.c_int, [vp, vp, vp, vp, i64, f32, f32, vp, sz, vp]),
             "pm_timing_enable": (ctypes.c_int, [ctypes.c_int]),
             "pm_timing_read": (ctypes.c_int, [ctypes.POINTER(PmLaunchTime), ctypes.c_int]),
         }
@@ -171,10 +181,18 @@ def stream_of(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def ns_form_code(ns_form) -> int:
+    """'standard' (torch's quintic) or 'gram' (PAN 2's gram form) -> pm_hparams.ns_form."""
+    if ns_form not in NS_FORMS:
+        raise ValueError(f"ns_form must be one of {sorted(NS_FORMS)}, got {ns_form!r}")
+    return NS_FORMS[ns_form]
+
+
 def make_hparams(*, momentum=0.95, nesterov=True, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5,
-                 eps=1e-7, weight_decay=0.0, workspace_limit=0):
+                 eps=1e-7, weight_decay=0.0, workspace_limit=0, ns_form="standard"):
     """PmHparams plus the ctypes array that must outlive the call (per-step coefficients)."""
     hp = PmHparams()
+    hp.ns_form = ns_form_code(ns_form)
     hp.momentum = float(momentum)
     hp.nesterov = 1 if nesterov else 0
     hp.ns_steps = int(ns_steps)
@@ -214,7 +232,7 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, nesterov, ns_coefficients,
-              ns_steps, eps, workspace_limit: int = 0) -> None:
+              ns_steps, eps, workspace_limit: int = 0, ns_form: str = "standard") -> None:
     """pm_muon_step over matching lists of 2-D device tensors (updated in place).
 
     lr: python float, or a 1-element float tensor on the same device (read on
@@ -242,7 +260,7 @@ def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, ne
         m.adj_ratio = float(r)
     hp, keep = make_hparams(momentum=momentum, nesterov=nesterov, ns_coefficients=ns_coefficients,
                             ns_steps=ns_steps, eps=eps, weight_decay=weight_decay,
-                            workspace_limit=workspace_limit)
+                            workspace_limit=workspace_limit, ns_form=ns_form)
     lr_dev, lr_host, lr_keep = None, 0.0, None
     if isinstance(lr, torch.Tensor):
         if lr.numel() != 1:
@@ -267,7 +285,7 @@ def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, ne
 
 
 def newton_schulz_into(pairs, *, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7,
-                       workspace_limit: int = 0) -> None:
+                       workspace_limit: int = 0, ns_form: str = "standard") -> None:
     """pm_newton_schulz over [(input, output)] pairs; outputs are bf16, same shape."""
     lib = load()
     n = len(pairs)
@@ -286,7 +304,7 @@ def newton_schulz_into(pairs, *, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_s
         m.in_ld, m.out_ld = _ld(x), _ld(o)
         m.in_dtype = dtype_code(x)
     hp, keep = make_hparams(ns_coefficients=ns_coefficients, ns_steps=ns_steps, eps=eps,
-                            workspace_limit=workspace_limit)
+                            workspace_limit=workspace_limit, ns_form=ns_form)
     with torch.cuda.device(dev):
         nbytes = lib.pm_ns_workspace_bytes(mats, n, ctypes.byref(hp))
         if nbytes == 0:
@@ -352,6 +370,30 @@ def gram(x: torch.Tensor) -> torch.Tensor:
         ws = workspace(nbytes, x.device)
         rc = lib.pm_gram(x.data_ptr(), rows, cols, out.data_ptr(), ws.data_ptr(), nbytes, stream_of(x.device))
     check(rc, "pm_gram")
+    return out
+
+
+def gemm_symmetric(left: torch.Tensor, right: torch.Tensor, addend: torch.Tensor | None = None, *,
+                   alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """alpha * left @ right.T + beta * addend through pm_gemm_symmetric (bf16, m x m,
+    m a multiple of 256; the upper triangle is computed and mirrored)."""
+    lib = load()
+    mats = [(left, "left"), (right, "right")] + ([(addend, "addend")] if addend is not None else [])
+    m = left.shape[0]
+    for t, w in mats:
+        _check_matrix(t, w)
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != (m, m):
+            raise ValueError(f"{w} must be a contiguous bf16 {m}x{m} matrix")
+    if beta != 0.0 and addend is None:
+        raise ValueError("beta != 0 needs an addend")
+    out = torch.empty((m, m), dtype=torch.bfloat16, device=left.device)
+    with torch.cuda.device(left.device):
+        nbytes = lib.pm_gemm_symmetric_workspace_bytes()
+        ws = workspace(nbytes, left.device)
+        rc = lib.pm_gemm_symmetric(left.data_ptr(), right.data_ptr(),
+                                   addend.data_ptr() if addend is not None else None, out.data_ptr(), m,
+                                   float(alpha), float(beta), ws.data_ptr(), nbytes, stream_of(left.device))
+    check(rc, "pm_gemm_symmetric")
     return out
 
 

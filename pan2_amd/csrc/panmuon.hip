@@ -43,6 +43,9 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 constexpr size_t kAlign = 256;
+// Largest extent: a 256-row operand panel of the padded long side spans
+// 256 * Np * 2 bytes, which a buffer descriptor's 32-bit size must cover.
+constexpr int kMaxExtent = (1 << 23) - kTile;
 constexpr uint64_t kDefaultWorkspaceLimit = 32ull << 30;  // 32 GiB
 
 size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
@@ -55,7 +58,11 @@ struct Plan {
   double flops;
 };
 
-Plan make_plan(int64_t rows, int64_t cols) {
+// Square Mp x Mp work matrices per matrix: A and B (standard form) or R, Z,
+// RZ and two Q (gram form).
+int square_bufs(int form) { return form == NS_GRAM ? 5 : 2; }
+
+Plan make_plan(int64_t rows, int64_t cols, int form) {
   Plan p{};
   p.rows = (int32_t)rows;
   p.cols = (int32_t)cols;
@@ -67,14 +74,22 @@ Plan make_plan(int64_t rows, int64_t cols) {
   const size_t x = align_up((size_t)p.Mp * p.Np * 2);
   const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
   const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);
-  p.ws = 4 * x + 2 * a + part + kAlign;
+  p.ws = 4 * x + (size_t)square_bufs(form) * a + part + kAlign;
   const double M = p.M, N = p.N;
   p.flops = M * (M + 1) * N + M * M * (M + 1) + 2 * M * M * N;
   return p;
 }
 
-// GEMM launches of one group: GRAM, POLY and UPDATE/FINAL per iteration.
-int gemm_launches(const pm_hparams* hp) { return 3 * hp->ns_steps; }
+// Iteration at which the gram form applies Q to X and recomputes the gram
+// (pan/optim/patch_muon.py:286: reset_iterations = {2} when ns_steps > 2), or -1.
+int gram_reset(int steps) { return steps > 2 ? 2 : -1; }
+
+// GEMM launches of one group (an upper bound for the gram form): standard =
+// GRAM, POLY and UPDATE/FINAL per iteration; gram = two grams, at most four
+// symmetric products per iteration, the apply at the reset and FINAL.
+int gemm_launches(const pm_hparams* hp) {
+  return hp->ns_form == NS_GRAM ? 4 * hp->ns_steps + 4 : 3 * hp->ns_steps;
+}
 
 // Descriptor table layout:
 //   descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1] | queues[launches][kXcds]
@@ -105,6 +120,8 @@ int check_hparams(const pm_hparams* hp) {
   if (!hp) return fail(PM_EINVAL, "hparams is NULL");
   if (hp->ns_steps < 1 || hp->ns_steps >= 100)
     return fail(PM_EUNSUPPORTED, "ns_steps must be in [1, 99], got %d", hp->ns_steps);
+  if (hp->ns_form != PM_NS_STANDARD && hp->ns_form != PM_NS_GRAM)
+    return fail(PM_EINVAL, "ns_form must be PM_NS_STANDARD or PM_NS_GRAM, got %d", hp->ns_form);
   if (!(hp->eps >= 0.0f)) return fail(PM_EINVAL, "eps must be >= 0");
   return PM_OK;
 }
@@ -112,7 +129,12 @@ int check_hparams(const pm_hparams* hp) {
 int check_extent(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return fail(PM_EINVAL, "matrix extents must be positive, got %lldx%lld",
                                           (long long)rows, (long long)cols);
-  if (rows > (1 << 30) || cols > (1 << 30) || rows * cols > (1ll << 40))
+  // 256 rows of the long side must stay within a 32-bit buffer descriptor
+  if (rows > kMaxExtent || cols > kMaxExtent)
+    return fail(PM_EUNSUPPORTED, "matrix %lldx%lld: each extent must be at most %d", (long long)rows,
+                (long long)cols, kMaxExtent);
+  // keeps every per-launch tile count and prefix sum within int32
+  if (rows * cols > (1ll << 40))
     return fail(PM_EINVAL, "matrix %lldx%lld is too large", (long long)rows, (long long)cols);
   return PM_OK;
 }
@@ -181,7 +203,10 @@ void timing_begin(hipStream_t stream) {
   if (!g_timing.on) return;
   hipEvent_t e = timing_event();
   if (!e) return;
-  hipEventRecord(e, stream);
+  if (hipEventRecord(e, stream) != hipSuccess) {
+    g_timing.pool.push_back(e);
+    return;
+  }
   g_timing.last = e;
   g_timing.last_stream = stream;
 }
@@ -191,7 +216,10 @@ void timing_mark(hipStream_t stream, int kind, int group, int iteration, int nma
   if (!g_timing.on || !g_timing.last || g_timing.last_stream != stream) return;
   hipEvent_t e = timing_event();
   if (!e) return;
-  hipEventRecord(e, stream);
+  if (hipEventRecord(e, stream) != hipSuccess) {
+    g_timing.pool.push_back(e);
+    return;
+  }
   TimingRec r{};
   r.info.kind = kind;
   r.info.group = group;
@@ -205,9 +233,142 @@ void timing_mark(hipStream_t stream, int kind, int group, int iteration, int nma
   g_timing.last = e;
 }
 
-// Runs one group: items[lo, hi) share the workspace `ws`.
+// Enqueues the GEMM and Q-init launches of one group. Every GEMM launch walks
+// all matrices of the group and takes the next set of queue counters.
+struct Launcher {
+  GemmArgs ga;          // shared fields (descs, n, mode, lr, wd) already set
+  const int32_t* sym;   // device prefix sums: symmetric (upper-triangle) tiles
+  const int32_t* full;  // device prefix sums: full tiles
+  int32_t sym_total, full_total, sym_grid, full_grid;
+  int32_t* queues;      // kXcds counters per GEMM launch, zero at upload
+  int launch = 0, max_launches = 0;
+  bool final_f32 = false;
+  hipStream_t stream;
+  int group, count;
+  double f_gram = 0, f_sym = 0, f_upd = 0;  // algorithmic FLOPs per launch kind (timing records)
+
+  int next_queues(GemmArgs& a) {
+    if (launch >= max_launches) return fail(PM_EINVAL, "internal: more GEMM launches than planned");
+    a.queues = queues + kXcds * launch++;
+    return PM_OK;
+  }
+  int gram(int cur, bool first, int sc, int it) {
+    GemmArgs a = ga;
+    a.stage = ST_GRAM; a.cur = cur; a.first = first; a.sc = sc;
+    a.prefix = sym; a.total = sym_total;
+    if (int rc = next_queues(a)) return rc;
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
+    timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
+    return check("gram launch");
+  }
+  // S[sc] = alpha·S[sl]·S[sr]ᵀ + beta·S[sd]
+  int symm(int sl, int sr, int sd, int sc, float alpha, float beta, int it) {
+    GemmArgs a = ga;
+    a.stage = ST_SYMM; a.sl = sl; a.sr = sr; a.sd = sd; a.sc = sc; a.c = alpha; a.b = beta;
+    a.prefix = sym; a.total = sym_total;
+    if (int rc = next_queues(a)) return rc;
+    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_SYMM>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
+    timing_mark(stream, PM_K_POLY, group, it, count, f_sym, 0.0);
+    return check("symmetric product launch");
+  }
+  // X' = s·(a·X + S[sl]·X) into the other X slot, or (last) the param step
+  int update(int sl, float coef_a, int cur, bool first, bool last, int it) {
+    GemmArgs a = ga;
+    a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = sl; a.a = coef_a; a.cur = cur; a.first = first;
+    a.prefix = full; a.total = full_total;
+    if (int rc = next_queues(a)) return rc;
+    if (last && final_f32)
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
+    else if (last)
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
+    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
+    return check("Newton-Schulz update launch");
+  }
+  int qinit(int sz, int sq, float coef_a, int max_mp, int it) {
+    for (int first = 0; first < count; first += 65535)  // gridDim.y limit
+      hipLaunchKernelGGL(pm_qinit_kernel, dim3(max_mp / kProTile, std::min(count - first, 65535)), dim3(kThreads), 0,
+                         stream, ga.descs, first, sz, sq, coef_a);
+    timing_mark(stream, PM_K_QINIT, group, it, count, 0.0, 0.0);
+    return check("Q init launch");
+  }
+  static int check(const char* what) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? PM_OK : hip_fail(e, what);
+  }
+};
+
+struct Coeffs {
+  const pm_hparams* hp;
+  Coeff at(int it) const {
+    if (hp->coeffs) return Coeff{hp->coeffs[3 * it], hp->coeffs[3 * it + 1], hp->coeffs[3 * it + 2]};
+    return Coeff{hp->a, hp->b, hp->c};
+  }
+};
+
+// Standard quintic (torch/optim/_muon.py:61-66): per iteration A = X Xᵀ,
+// B = b A + c A², X <- a X + B X; the last update is fused with the step.
+int run_standard(Launcher& L, const pm_hparams* hp) {
+  const Coeffs co{hp};
+  for (int it = 0; it < hp->ns_steps; ++it) {
+    const Coeff k = co.at(it);
+    const int cur = it & 1;
+    int rc = L.gram(cur, it == 0, /*A*/ 0, it);
+    if (!rc) rc = L.symm(0, 0, 0, /*B*/ 1, k.c, k.b, it);
+    if (!rc) rc = L.update(/*B*/ 1, k.a, cur, it == 0, it + 1 == hp->ns_steps, it);
+    if (rc) return rc;
+  }
+  return PM_OK;
+}
+
+// Gram form of PAN 2 (_gram_newtonschulz_local, pan/optim/patch_muon.py:275-334):
+// R = X Xᵀ; per iteration Z = c R R + b R; Q = a I + Z (first of a segment)
+// or Q Z + a Q; R <- (aI+Z) R (aI+Z) as RZ = R Z + a R, R = Z RZ + a RZ
+// (skipped before a reset and after the last iteration); at the reset
+// iteration X <- Q X and R = X Xᵀ again; finally X <- Q X, fused with the step.
+// The Frobenius scaling of X is folded as in the standard form: into the first
+// gram (s²) and into the first application of Q to the unscaled X (s).
+int run_gram(Launcher& L, const pm_hparams* hp, int max_mp) {
+  enum { R = 0, Z = 1, RZ = 2, Q0 = 3, Q1 = 4 };
+  const Coeffs co{hp};
+  const int steps = hp->ns_steps, reset = gram_reset(steps);
+  int cur = 0;          // X slot holding the current X
+  bool scaled = false;  // has X been scaled by 1/‖X‖ yet?
+  int q = -1;           // square buffer holding Q (-1: no Q in this segment)
+  int rc = L.gram(cur, true, R, 0);
+  for (int it = 0; it < steps && !rc; ++it) {
+    const Coeff k = co.at(it);
+    if (it == reset) {
+      rc = L.update(q, 0.0f, cur, !scaled, false, it);
+      cur ^= 1;
+      scaled = true;
+      if (!rc) rc = L.gram(cur, false, R, it);
+      q = -1;
+    }
+    if (!rc) rc = L.symm(R, R, R, Z, k.c, k.b, it);
+    if (rc) break;
+    if (q < 0) {
+      rc = L.qinit(Z, Q0, k.a, max_mp, it);
+      q = Q0;
+    } else {
+      const int qn = q == Q0 ? Q1 : Q0;
+      rc = L.symm(q, Z, q, qn, 1.0f, k.a, it);
+      q = qn;
+    }
+    if (!rc && it + 1 < steps && it + 1 != reset) {
+      rc = L.symm(R, Z, R, RZ, 1.0f, k.a, it);
+      if (!rc) rc = L.symm(Z, RZ, RZ, R, 1.0f, k.a, it);
+    }
+  }
+  if (!rc) rc = L.update(q, 0.0f, cur, !scaled, true, steps - 1);
+  return rc;
+}
+
+// Runs one group: items[0, count) share the workspace `ws`.
 int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
               double lr_host, char* ws, hipStream_t stream) {
+  const int form = hp->ns_form;
   // Table first, then per-matrix buffers.
   const size_t tb = table_bytes(count, gemm_launches(hp));
   char* cursor = ws + tb;
@@ -218,6 +379,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   int32_t* full = (int32_t*)((char*)sym + align_up((size_t)(count + 1) * 4));
   const int32_t* queues = (const int32_t*)((char*)full + align_up((size_t)(count + 1) * 4));  // zeros
   pro[0] = sym[0] = full[0] = 0;
+  int max_mp = 0;
   for (int i = 0; i < count; ++i) {
     Item& it = items[i];
     const Plan& p = it.plan;
@@ -230,8 +392,10 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     d.X[1] = (uint16_t*)cursor; cursor += x;
     d.XT[0] = (uint16_t*)cursor; cursor += x;
     d.XT[1] = (uint16_t*)cursor; cursor += x;
-    d.A = (uint16_t*)cursor; cursor += a;
-    d.B = (uint16_t*)cursor; cursor += a;
+    for (int b = 0; b < kSquareBufs; ++b) {
+      d.S[b] = b < square_bufs(form) ? (uint16_t*)cursor : nullptr;
+      if (b < square_bufs(form)) cursor += a;
+    }
     d.partials = (float*)cursor; cursor += align_up((size_t)pro_tiles(p) * 4);
     d.scales = (float*)cursor; cursor += kAlign;
     d.pro_tiles = pro_tiles(p);
@@ -239,18 +403,19 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     pro[i + 1] = pro[i] + pro_tiles(p);
     sym[i + 1] = sym[i] + sym_tiles(p);
     full[i + 1] = full[i] + full_tiles(p);
+    max_mp = std::max(max_mp, p.Mp);
   }
   int rc = upload(host.data(), tb, ws, stream);
   if (rc) return rc;
   timing_begin(stream);
 
   // Algorithmic work per launch (timing records only).
-  double f_gram = 0, f_poly = 0, f_upd = 0, b_pro = 0;
+  double f_gram = 0, f_sym = 0, f_upd = 0, b_pro = 0;
   for (int i = 0; i < count; ++i) {
     const Plan& p = items[i].plan;
     const double M = p.M, N = p.N, elems = M * N;
     f_gram += M * (M + 1) * N;
-    f_poly += M * M * (M + 1);
+    f_sym += M * M * (M + 1);
     f_upd += 2 * M * M * N;
     const MatDesc& d = items[i].desc;
     const double gb = d.g_dt == PM_DTYPE_F32 ? 4 : 2;
@@ -274,52 +439,33 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
 
   // The FINAL epilogue is compiled per param dtype; run_all keeps a group's
   // params of one dtype (MODE_NS writes bf16).
-  const bool final_f32 = mode == MODE_STEP && items[0].desc.p_dt == PM_DTYPE_F32;
   for (int i = 1; i < count; ++i)
     if (mode == MODE_STEP && items[i].desc.p_dt != items[0].desc.p_dt)
       return fail(PM_EINVAL, "internal: a group mixes param dtypes");
 
-  GemmArgs ga{};
-  ga.descs = ddesc;
-  ga.n = count;
-  ga.mode = mode;
-  ga.lr_dev = lr_dev;
-  ga.wd = (float)hp->weight_decay;
-  ga.wdf_host = (float)(1.0 - lr_host * (double)hp->weight_decay);
-  const int sym_grid = gemm_grid(sym[count]), full_grid = gemm_grid(full[count]);
-  int launch = 0;  // queue counters: one set of kXcds per launch
-  for (int it = 0; it < hp->ns_steps; ++it) {
-    Coeff k{hp->a, hp->b, hp->c};
-    if (hp->coeffs) k = Coeff{hp->coeffs[3 * it], hp->coeffs[3 * it + 1], hp->coeffs[3 * it + 2]};
-    ga.a = k.a; ga.b = k.b; ga.c = k.c;
-    ga.cur = it & 1;
-    ga.first = it == 0;
-    ga.prefix = dsym;
-    ga.total = sym[count];
-    ga.stage = ST_GRAM;
-    ga.queues = dqueues + kXcds * launch++;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, ga);
-    timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
-    ga.stage = ST_POLY;
-    ga.queues = dqueues + kXcds * launch++;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_POLY>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, ga);
-    timing_mark(stream, PM_K_POLY, group, it, count, f_poly, 0.0);
-    ga.prefix = dfull;
-    ga.total = full[count];
-    const bool last = it + 1 == hp->ns_steps;
-    ga.stage = last ? ST_FINAL : ST_UPDATE;
-    ga.queues = dqueues + kXcds * launch++;
-    if (last && final_f32)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32>), dim3(full_grid), dim3(kGemmThreads), 0, stream, ga);
-    else if (last)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16>), dim3(full_grid), dim3(kGemmThreads), 0, stream, ga);
-    else
-      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full_grid), dim3(kGemmThreads), 0, stream, ga);
-    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
-    e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "Newton-Schulz launch");
-  }
-  return PM_OK;
+  Launcher L{};
+  L.ga.descs = ddesc;
+  L.ga.n = count;
+  L.ga.mode = mode;
+  L.ga.lr_dev = lr_dev;
+  L.ga.wd = (float)hp->weight_decay;
+  L.ga.wdf_host = (float)(1.0 - lr_host * (double)hp->weight_decay);
+  L.sym = dsym;
+  L.full = dfull;
+  L.sym_total = sym[count];
+  L.full_total = full[count];
+  L.sym_grid = gemm_grid(sym[count]);
+  L.full_grid = gemm_grid(full[count]);
+  L.queues = dqueues;
+  L.max_launches = gemm_launches(hp);
+  L.final_f32 = mode == MODE_STEP && items[0].desc.p_dt == PM_DTYPE_F32;
+  L.stream = stream;
+  L.group = group;
+  L.count = count;
+  L.f_gram = f_gram;
+  L.f_sym = f_sym;
+  L.f_upd = f_upd;
+  return form == NS_GRAM ? run_gram(L, hp, max_mp) : run_standard(L, hp);
 }
 
 // Sorts items by descending work (longest tiles first), packs them into
@@ -367,7 +513,7 @@ size_t plan_workspace(const std::vector<Plan>& plans, const pm_hparams* hp) {
   return table_bytes((int)plans.size(), gemm_launches(hp)) + body;
 }
 
-int collect_step(const pm_matrix* mats, int n, std::vector<Item>& items) {
+int collect_step(const pm_matrix* mats, int n, int form, std::vector<Item>& items) {
   if (n < 0 || (n > 0 && !mats)) return fail(PM_EINVAL, "bad matrix list");
   items.clear();
   items.reserve(n);
@@ -381,7 +527,7 @@ int collect_step(const pm_matrix* mats, int n, std::vector<Item>& items) {
     if (m.param_ld < m.cols || m.grad_ld < m.cols || m.momentum_ld < m.cols)
       return fail(PM_EINVAL, "matrix %d: row stride smaller than cols", i);
     Item it{};
-    it.plan = make_plan(m.rows, m.cols);
+    it.plan = make_plan(m.rows, m.cols, form);
     MatDesc& d = it.desc;
     d.param = m.param; d.grad = m.grad; d.mom = m.momentum;
     d.p_ld = m.param_ld; d.g_ld = m.grad_ld; d.m_ld = m.momentum_ld;
@@ -392,7 +538,7 @@ int collect_step(const pm_matrix* mats, int n, std::vector<Item>& items) {
   return PM_OK;
 }
 
-int collect_ns(const pm_ns_matrix* mats, int n, std::vector<Item>& items) {
+int collect_ns(const pm_ns_matrix* mats, int n, int form, std::vector<Item>& items) {
   if (n < 0 || (n > 0 && !mats)) return fail(PM_EINVAL, "bad matrix list");
   items.clear();
   items.reserve(n);
@@ -404,7 +550,7 @@ int collect_ns(const pm_ns_matrix* mats, int n, std::vector<Item>& items) {
     if (!valid_dtype(m.in_dtype)) return fail(PM_EDTYPE, "matrix %d: input dtype must be f32 or bf16", i);
     if (m.in_ld < m.cols || m.out_ld < m.cols) return fail(PM_EINVAL, "matrix %d: row stride smaller than cols", i);
     Item it{};
-    it.plan = make_plan(m.rows, m.cols);
+    it.plan = make_plan(m.rows, m.cols, form);
     MatDesc& d = it.desc;
     d.param = m.out; d.grad = m.in; d.mom = nullptr;
     d.p_ld = m.out_ld; d.g_ld = m.in_ld; d.m_ld = 0;
@@ -430,7 +576,7 @@ const char* pm_last_error(void) { return g_err.c_str(); }
 size_t pm_workspace_bytes(const pm_matrix* mats, int n, const pm_hparams* hp) {
   if (check_hparams(hp)) return 0;
   std::vector<Item> items;
-  if (collect_step(mats, n, items)) return 0;
+  if (collect_step(mats, n, hp->ns_form, items)) return 0;
   std::vector<Plan> plans;
   for (auto& it : items) plans.push_back(it.plan);
   return plan_workspace(plans, hp);
@@ -439,7 +585,7 @@ size_t pm_workspace_bytes(const pm_matrix* mats, int n, const pm_hparams* hp) {
 size_t pm_ns_workspace_bytes(const pm_ns_matrix* mats, int n, const pm_hparams* hp) {
   if (check_hparams(hp)) return 0;
   std::vector<Item> items;
-  if (collect_ns(mats, n, items)) return 0;
+  if (collect_ns(mats, n, hp->ns_form, items)) return 0;
   std::vector<Plan> plans;
   for (auto& it : items) plans.push_back(it.plan);
   return plan_workspace(plans, hp);
@@ -451,7 +597,7 @@ int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp, const float
   int rc = check_hparams(hp);
   if (rc) return rc;
   std::vector<Item> items;
-  rc = collect_step(mats, n, items);
+  rc = collect_step(mats, n, hp->ns_form, items);
   if (rc) return rc;
   // Items are still in caller order here. The host-lr product stays in double
   // and is rounded once, as the reference passes -adjusted_lr to its kernel.
@@ -465,7 +611,7 @@ int pm_newton_schulz(const pm_ns_matrix* mats, int n, const pm_hparams* hp, void
   int rc = check_hparams(hp);
   if (rc) return rc;
   std::vector<Item> items;
-  rc = collect_ns(mats, n, items);
+  rc = collect_ns(mats, n, hp->ns_form, items);
   if (rc) return rc;
   return run_all(items, hp, MODE_NS, nullptr, 0.0, workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -548,7 +694,7 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   std::vector<char> host(table_bytes(1, 1), 0);
   MatDesc* d = (MatDesc*)host.data();
   d->X[0] = (uint16_t*)x;
-  d->A = (uint16_t*)out;
+  d->S[0] = (uint16_t*)out;
   d->Mp = d->M = (int32_t)rows;
   d->Np = d->N = (int32_t)cols;
   d->rows = (int32_t)rows;
@@ -570,9 +716,56 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   ga.stage = ST_GRAM;
   ga.cur = 0;
   ga.first = 0;
+  ga.sc = 0;
   hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PM_OK : hip_fail(e, "gram launch");
+}
+
+size_t pm_gemm_symmetric_workspace_bytes(void) { return table_bytes(1, 1); }
+
+int pm_gemm_symmetric(const void* left, const void* right, const void* addend, void* out, int64_t m, float alpha,
+                      float beta, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_extent(m, m);
+  if (rc) return rc;
+  if (!left || !right || !out || !workspace) return fail(PM_EINVAL, "NULL pointer");
+  if (beta != 0.0f && !addend) return fail(PM_EINVAL, "addend is NULL but beta != 0");
+  if (m % kTile) return fail(PM_EINVAL, "pm_gemm_symmetric needs m to be a multiple of 256");
+  if (workspace_bytes < table_bytes(1, 1)) return fail(PM_EWORKSPACE, "workspace too small");
+  if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
+  std::vector<char> host(table_bytes(1, 1), 0);
+  MatDesc* d = (MatDesc*)host.data();
+  d->S[0] = (uint16_t*)left;
+  d->S[1] = (uint16_t*)right;
+  d->S[2] = (uint16_t*)(addend ? addend : left);  // not read when beta == 0
+  d->S[3] = (uint16_t*)out;
+  d->Mp = d->M = d->Np = d->N = (int32_t)m;
+  d->rows = d->cols = (int32_t)m;
+  int32_t* sym = (int32_t*)(host.data() + align_up(sizeof(MatDesc)) + align_up(8));
+  const size_t queues_off = align_up(sizeof(MatDesc)) + 3 * align_up(8);  // one launch's counters, zeros
+  const int32_t nt = (int32_t)(m / kTile);
+  sym[0] = 0;
+  sym[1] = nt * (nt + 1) / 2;
+  hipStream_t s = (hipStream_t)stream;
+  rc = upload(host.data(), host.size(), workspace, s);
+  if (rc) return rc;
+  GemmArgs ga{};
+  ga.descs = (const MatDesc*)workspace;
+  ga.prefix = (const int32_t*)((char*)workspace + ((char*)sym - host.data()));
+  ga.queues = (int32_t*)((char*)workspace + queues_off);
+  ga.total = sym[1];
+  ga.n = 1;
+  ga.stage = ST_SYMM;
+  ga.sl = 0;
+  ga.sr = 1;
+  ga.sd = 2;
+  ga.sc = 3;
+  ga.c = alpha;
+  ga.b = beta;
+  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_SYMM>, dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "symmetric product launch");
 }
 
 }  // extern "C"

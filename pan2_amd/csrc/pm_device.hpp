@@ -26,7 +26,12 @@ constexpr int kGemmThreads = 512;  // GEMM blocks: 8 waves, two per SIMD
 constexpr int kProTile = 64;     // prologue tile edge
 
 enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
-enum Stage : int32_t { ST_GRAM = 0, ST_POLY = 1, ST_UPDATE = 2, ST_FINAL = 3 };
+// GRAM: S[sc] = X Xᵀ. SYMM: S[sc] = alpha·S[sl]·S[sr]ᵀ + beta·S[sd] (symmetric
+// result). UPDATE / FINAL: X' = a·X + S[sl]·X (FINAL fused with the param step).
+enum Stage : int32_t { ST_GRAM = 0, ST_SYMM = 1, ST_UPDATE = 2, ST_FINAL = 3 };
+// Newton–Schulz organisation of a call (pm_hparams.ns_form).
+enum NsForm : int32_t { NS_STANDARD = 0, NS_GRAM = 1 };
+constexpr int kSquareBufs = 5;  // Mp x Mp bf16 work matrices per matrix (the gram form uses all five)
 enum Mode : int32_t { MODE_STEP = 0, MODE_NS = 1 };
 
 // Per-matrix descriptor, resident in the workspace for the duration of a call.
@@ -46,8 +51,10 @@ struct MatDesc {
   // workspace buffers
   uint16_t* X[2];     // bf16 Mp x Np (ld Np), ping-pong
   uint16_t* XT[2];    // bf16 Np x Mp (ld Mp), same values transposed
-  uint16_t* A;        // bf16 Mp x Mp gram
-  uint16_t* B;        // bf16 Mp x Mp polynomial b A + c A²
+  // bf16 Mp x Mp work matrices. Standard form: S[0] = A = X Xᵀ,
+  // S[1] = B = b A + c A². Gram form: S[0] = R, S[1] = Z, S[2] = R Z + a R,
+  // S[3], S[4] = Q (ping-pong). Unused entries are null.
+  uint16_t* S[kSquareBufs];
   float* partials;    // Σx² of each prologue tile
   float* scales;      // [0] = 1/max(‖X‖,eps)², [1] = 1/max(‖X‖,eps)
   int32_t pro_tiles;
@@ -73,7 +80,8 @@ struct GemmArgs {
   int32_t cur;            // which X/XT ping-pong buffer holds the current X
   int32_t first;          // iteration 0: fold the Frobenius normalisation
   int32_t mode;
-  float a, b, c;
+  int32_t sl, sr, sd, sc;  // square-buffer operands: left, right, addend, output
+  float a, b, c;           // UPDATE / FINAL: a; SYMM: alpha = c, beta = b
   const float* lr_dev;    // device lr, or null
   float wd;               // weight decay (device-lr path)
   float wdf_host;         // 1 - lr*wd (host-lr path)

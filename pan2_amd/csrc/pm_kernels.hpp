@@ -461,25 +461,29 @@ struct TileJob {
 };
 
 template <int STAGE, class D>
-__device__ __forceinline__ TileJob decode_tile(const D& d, int lt, int cur) {
+__device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArgs& args) {
   TileJob j;
   int P, Q;
   bool sym = false;
+  const int cur = args.cur;
   if (STAGE == ST_GRAM) {
     j.L = j.R = d.X[cur]; j.ldl = j.ldr = d.Np; j.K = d.Np; P = Q = d.Mp; sym = true;
-  } else if (STAGE == ST_POLY) {
-    j.L = j.R = d.A; j.ldl = j.ldr = d.Mp; j.K = d.Mp; P = Q = d.Mp; sym = true;
+  } else if (STAGE == ST_SYMM) {
+    // S[sl] · S[sr]ᵀ: both operands are read by rows (a symmetric right operand
+    // is its own transpose)
+    j.L = d.S[args.sl]; j.R = d.S[args.sr]; j.ldl = j.ldr = d.Mp; j.K = d.Mp; P = Q = d.Mp; sym = true;
   } else if (STAGE == ST_UPDATE) {
-    // C (Mp x Np) = B · X, X supplied as Xᵀ rows
-    j.L = d.B; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
+    // C (Mp x Np) = S[sl] · X, X supplied as Xᵀ rows
+    j.L = d.S[args.sl]; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
   } else if (!d.trans) {
-    // wide FINAL: C (Np x Mp) = Xᵀ · B = (B X)ᵀ, so a lane's quad (4 tile rows
-    // at one tile column) is 4 consecutive columns of one param row
-    j.L = d.XT[cur]; j.ldl = d.Mp; j.R = d.B; j.ldr = d.Mp; j.K = d.Mp; P = d.Np; Q = d.Mp;
+    // wide FINAL: C (Np x Mp) = Xᵀ · S[sl] = (S[sl] X)ᵀ (S[sl] is symmetric), so
+    // a lane's quad (4 tile rows at one tile column) is 4 consecutive columns
+    // of one param row
+    j.L = d.XT[cur]; j.ldl = d.Mp; j.R = d.S[args.sl]; j.ldr = d.Mp; j.K = d.Mp; P = d.Np; Q = d.Mp;
   } else {
-    // tall FINAL: C (Mp x Np) = B · X, whose transpose is the param: a quad is
-    // again 4 consecutive columns of one param row
-    j.L = d.B; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
+    // tall FINAL: C (Mp x Np) = S[sl] · X, whose transpose is the param: a quad
+    // is again 4 consecutive columns of one param row
+    j.L = d.S[args.sl]; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
   }
   if (sym) {
     sym_tile(lt, P / kTile, j.ti, j.tj);
@@ -522,6 +526,32 @@ __device__ __forceinline__ u32x4 pair_rows(u16x4 a, u16x4 b) {
   const auto s0 = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
   const auto s1 = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
   return (u32x4){s0[0], s1[0], s0[1], s1[1]};
+}
+
+// Diagonal tiles of a symmetric product whose operands differ: the stores keep
+// the elements on and above the diagonal (store_upper4: element e of v is
+// column col0 + e of `row`) and mirror the strict upper part (store_lower8:
+// element e of v is the output element (p0 + e, q), stored at C[q][p0 + e]),
+// so the tile comes out exactly symmetric.
+__device__ __forceinline__ void store_upper4(uint16_t* dst, u16x4 v, int col0, int row) {
+  if (col0 >= row) {
+    *(u16x4*)dst = v;
+    return;
+  }
+  if (col0 + 3 < row) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (col0 + e >= row) dst[e] = v[e];
+}
+__device__ __forceinline__ void store_lower8(uint16_t* dst, u32x4 v, int p0, int q) {
+  if (p0 + 7 < q) {
+    *(u32x4*)dst = v;
+    return;
+  }
+  if (p0 >= q) return;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (p0 + e < q) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
 }
 
 // Loads, for every quad of this lane, the 4 consecutive elements T[q][p0..p0+3]
@@ -583,14 +613,18 @@ __device__ __forceinline__ int xcc_id() {
 }
 
 // One Newton–Schulz stage over every matrix of the group.
-//   GRAM   A = s·X Xᵀ            (s = 1/‖X‖² at iteration 0, folding
-//                                 X.div_(norm) of torch/optim/_muon.py:59)
-//   POLY   B = c·A A + b·A        (torch.addmm(A, A, A, beta=b, alpha=c), :63-65)
-//   UPDATE X' = s·(a·X + B X)     (torch.addmm(X, B, X, beta=a), :66), written
-//                                 as X' and X'ᵀ
-//   FINAL  O = bf16(s·(a·X + B X)) then p <- p·(1-lr·wd) - lr·adj·O
+//   GRAM   S[sc] = s·X Xᵀ          (s = 1/‖X‖² when `first`, folding
+//                                   X.div_(norm) of torch/optim/_muon.py:59)
+//   SYMM   S[sc] = c·S[sl] S[sr]ᵀ + b·S[sd]
+//          standard form: B = c·A A + b·A (torch.addmm(A, A, A, beta=b,
+//          alpha=c), :63-65); gram form: the quack gemm_symmetric(_out)
+//          products of pan/optim/patch_muon.py:320-331
+//   UPDATE X' = s·(a·X + S[sl] X)  (torch.addmm(X, B, X, beta=a), :66; a = 0 is
+//                                   the gram form's X <- Q X, :316), written
+//                                   as X' and X'ᵀ
+//   FINAL  O = bf16(s·(a·X + S[sl] X)) then p <- p·(1-lr·wd) - lr·adj·O
 //          (pan/optim/muon_triton.py:130-131), or O stored (MODE_NS)
-// GRAM and POLY are symmetric: only upper-triangle tiles are computed and
+// GRAM and SYMM are symmetric: only upper-triangle tiles are computed and
 // each off-diagonal tile is also stored transposed. Every result is rounded
 // to bf16 where torch rounds it.
 // PDT is the param dtype of the FINAL epilogue (one instantiation per dtype
@@ -608,14 +642,28 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   // whose rows run along this lane's 4 consecutive output rows p: A is
   // symmetric, and X / Xᵀ hold the same values transposed. All loads are
   // issued before any store, so no load waits behind stores in vmcnt order.
-  if (STAGE == ST_GRAM || STAGE == ST_POLY) {
-    uint16_t* C = (STAGE == ST_GRAM) ? d.A : d.B;
+  if (STAGE == ST_GRAM || STAGE == ST_SYMM) {
+    uint16_t* C = d.S[args.sc];
     const int64_t ldc = d.Mp;
     const float s = (STAGE == ST_GRAM && args.first) ? d.scales[0] : 1.0f;
     const float cb = args.b, cc = args.c;
     const bool mirror = job.ti != job.tj;
+    // A diagonal tile of L·Rᵀ with L != R is symmetric only up to rounding:
+    // SYMM stores its upper part and mirrors it, so every symmetric product
+    // is exactly symmetric (later products read R and the addend through
+    // their transposes). A GRAM diagonal tile is bitwise symmetric already
+    // (the same products in the same order), and so is SYMM's when L == R.
+    const bool diag = STAGE == ST_SYMM && !mirror;
     u16x4 av[kQuads];
-    if (STAGE == ST_POLY) load_quads(av, d.A, ldc, pbase, qbase, lane);
+    if (STAGE == ST_SYMM) {
+      // the addend is symmetric, so its quads can be read from either orientation
+      if (cb != 0.0f) {
+        load_quads(av, d.S[args.sd], ldc, pbase, qbase, lane);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kQuads; ++i) av[i] = (u16x4){0, 0, 0, 0};
+      }
+    }
     const int g1 = (lane >> 4) & 1;
 #pragma unroll
     for (int mi = 0; mi < kMi; ++mi)
@@ -631,10 +679,23 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
             const float x = acc[mi][ni + h][r];
             o[h][r] = f2bf((STAGE == ST_GRAM) ? x * s : cc * x + cb * bf2f(av[i][r]));
           }
-          *(u16x4*)(C + (int64_t)(p0 + (lane & 3)) * ldc + (q & ~3)) = quad_transpose(o[h], lane);
+          const u16x4 t = quad_transpose(o[h], lane);
+          uint16_t* dst = C + (int64_t)(p0 + (lane & 3)) * ldc + (q & ~3);
+          if (!diag) {
+            *(u16x4*)dst = t;
+          } else {
+            store_upper4(dst, t, q & ~3, p0 + (lane & 3));
+          }
         }
-        if (mirror)
-          *(u32x4*)(C + (int64_t)(qbase + (ni + g1) * 16) * ldc + p0 - 4 * g1) = pair_rows(o[0], o[1]);
+        if (mirror || diag) {
+          const int qm = qbase + (ni + g1) * 16, pm = p0 - 4 * g1;
+          const u32x4 m = pair_rows(o[0], o[1]);
+          if (mirror) {
+            *(u32x4*)(C + (int64_t)qm * ldc + pm) = m;
+          } else {
+            store_lower8(C + (int64_t)qm * ldc + pm, m, pm, qm);
+          }
+        }
       }
     return;
   }
@@ -646,7 +707,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
     uint16_t* XTn = d.XT[cur ^ 1];
     const int64_t ldx = d.Np, ldxt = d.Mp;
     u16x4 xv[kQuads];
-    load_quads(xv, d.XT[cur], ldxt, pbase, qbase, lane);  // X[p][q] = Xᵀ[q][p]
+    if (ca != 0.0f) {
+      load_quads(xv, d.XT[cur], ldxt, pbase, qbase, lane);  // X[p][q] = Xᵀ[q][p]
+    } else {
+#pragma unroll
+      for (int i = 0; i < kQuads; ++i) xv[i] = (u16x4){0, 0, 0, 0};
+    }
     const int g1 = (lane >> 4) & 1;
 #pragma unroll
     for (int mi = 0; mi < kMi; ++mi)
@@ -706,7 +772,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
       for (int j = 0; j < kNi; ++j) {
         const int c0 = pbase + (b0 + bi) * 16, r = qbase + j * 16;  // param row r, columns c0..c0+3
-        xv[bi][j] = *(const u16x4*)(T + (int64_t)r * ldt + c0);
+        xv[bi][j] = (ca != 0.0f) ? *(const u16x4*)(T + (int64_t)r * ldt + c0) : (u16x4){0, 0, 0, 0};
         if (!step) continue;
         const bool in_row = r < prow;
         typedef typename PickVec<f32p>::elem E;
@@ -795,7 +861,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   int slot = 1;
 
   int m = find_matrix(prefix, args.n, t);
-  TileJob job = decode_tile<STAGE>(descs[m], t - prefix[m], args.cur);
+  TileJob job = decode_tile<STAGE>(descs[m], t - prefix[m], args);
   gemm_prefetch(make_engine(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl,
                             job.R + (int64_t)job.tj * kTile * job.ldr, job.ldr, wave),
                 ring);
@@ -810,7 +876,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     TileJob jn{};
     if (tn >= 0) {
       mn = find_matrix(prefix, args.n, tn);
-      jn = decode_tile<STAGE>(descs[mn], tn - prefix[mn], args.cur);
+      jn = decode_tile<STAGE>(descs[mn], tn - prefix[mn], args);
       gemm_prefetch(make_engine(jn.L + (int64_t)jn.ti * kTile * jn.ldl, jn.ldl,
                                 jn.R + (int64_t)jn.tj * kTile * jn.ldr, jn.ldr, wave),
                     ring);
@@ -825,6 +891,34 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     m = mn;
     job = jn;
     slot ^= 1;
+  }
+}
+
+// ============================================================ gram-form Q init
+// Q = Z + a·I for every matrix of the group: the first polynomial of a
+// gram-form segment, pan/optim/patch_muon.py:321-324 (Q = Z.clone(), then a
+// is added to the diagonal in bf16). Block (x, y) copies the 64-row band x of
+// matrix first + y; the padding rows and columns (beyond M) stay zero.
+__global__ __launch_bounds__(kThreads) void pm_qinit_kernel(const MatDesc* descs, int32_t first, int32_t sz,
+                                                            int32_t sq, float a) {
+#pragma clang fp contract(off)
+  const MatDesc& d = descs[first + blockIdx.y];
+  const int r0 = blockIdx.x * kProTile;
+  if (r0 >= d.Mp) return;
+  const uint16_t* Z = d.S[sz];
+  uint16_t* Q = d.S[sq];
+  const int runs = d.Mp / 8;  // 16-byte runs per row
+  for (int i = threadIdx.x; i < kProTile * runs; i += kThreads) {
+    const int r = r0 + i / runs, c0 = (i % runs) * 8;
+    u32x4 v = *(const u32x4*)(Z + (int64_t)r * d.Mp + c0);
+    const int e = r - c0;  // the diagonal element's place in this run, if any
+    if (r < d.M && e >= 0 && e < 8) {
+      const uint32_t w = v[e >> 1];
+      const uint16_t z = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+      const uint32_t q = f2bf(bf2f(z) + a);
+      v[e >> 1] = (e & 1) ? ((w & 0xffffu) | (q << 16)) : ((w & 0xffff0000u) | q);
+    }
+    *(u32x4*)(Q + (int64_t)r * d.Mp + c0) = v;
   }
 }
 

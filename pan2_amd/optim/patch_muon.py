@@ -48,6 +48,10 @@ def _is_dtensor(t) -> bool:
 # libpanmuon's workspace cap in bytes; 0 = the library default (32 GiB).
 WORKSPACE_LIMIT = 0
 
+# Newton–Schulz organisation: "standard" (torch's quintic, TORCH/optim/_muon.py:61-66)
+# or "gram" (PAN 2's _gram_newtonschulz_local, pan/optim/patch_muon.py:275-334).
+NS_FORM = "standard"
+
 
 @torch.compiler.disable
 def _single_tensor_muon(
@@ -125,7 +129,7 @@ def _single_tensor_muon(
             [ratios[i] for i in idx],
             lr=lr, weight_decay=weight_decay, momentum=momentum, nesterov=nesterov,
             ns_coefficients=ns_coefficients, ns_steps=ns_steps, eps=eps,
-            workspace_limit=WORKSPACE_LIMIT,
+            workspace_limit=WORKSPACE_LIMIT, ns_form=NS_FORM,
         )
 
 
@@ -148,15 +152,22 @@ def newton_schulz(grad: Tensor, ns_coefficients, ns_steps: int, eps: float) -> T
     flat_out = out.view(-1, *x.shape[-2:])
     _lib.newton_schulz_into([(flat_in[i], flat_out[i]) for i in range(flat_in.shape[0])],
                             ns_coefficients=ns_coefficients, ns_steps=ns_steps, eps=eps,
-                            workspace_limit=WORKSPACE_LIMIT)
+                            workspace_limit=WORKSPACE_LIMIT, ns_form=NS_FORM)
     return out
 
 
-def patch_muon() -> None:
+def patch_muon(ns_form: str | None = None) -> None:
     """Install the HIP path into torch.optim._muon (pan/optim/patch_muon.py:337-339).
 
+    ``ns_form`` selects the Newton–Schulz organisation for every later step:
+    "standard" (torch's quintic) or "gram" (the reference's production
+    _gram_newtonschulz_local); None keeps the current choice (``NS_FORM``).
     Loads libpanmuon first, so a missing or broken build fails here, loudly.
     """
+    global NS_FORM
+    if ns_form is not None:
+        _lib.ns_form_code(ns_form)  # validates
+        NS_FORM = ns_form
     _lib.load()
     torch.optim._muon._single_tensor_muon = _single_tensor_muon
     torch.optim._muon._zeropower_via_newtonschulz = newton_schulz

@@ -162,6 +162,31 @@ def test_elementwise_and_gram_argument_errors(lib):
     assert lib.pm_timing_read(None, 0) == 0
 
 
+def test_ns_form_and_extent_validation(lib):
+    assert step(lib, [mat()], hparams(ns_form="gram"), ws_bytes=4096) == _lib.PM_EWORKSPACE  # form accepted
+    hp = hparams()
+    hp.ns_form = 7
+    assert step(lib, [mat()], hp) == _lib.PM_EINVAL
+    assert "ns_form" in _lib.last_error()
+    with pytest.raises(ValueError, match="ns_form"):
+        _lib.ns_form_code("quintic")
+    # 256 rows of the padded long side must fit a 32-bit buffer descriptor
+    assert step(lib, [mat(rows=256, cols=(1 << 23))]) == _lib.PM_EUNSUPPORTED
+    assert "at most" in _lib.last_error()
+
+
+def test_gemm_symmetric_argument_errors(lib):
+    ws = lib.pm_gemm_symmetric_workspace_bytes()
+    assert ws > 0
+    assert lib.pm_gemm_symmetric(FAKE, FAKE, FAKE, FAKE, 320, 1.0, 0.5, FAKE, ws, None) == _lib.PM_EINVAL
+    assert "multiple of 256" in _lib.last_error()
+    assert lib.pm_gemm_symmetric(FAKE, FAKE, None, FAKE, 256, 1.0, 0.5, FAKE, ws, None) == _lib.PM_EINVAL
+    assert "addend" in _lib.last_error()
+    assert lib.pm_gemm_symmetric(None, FAKE, FAKE, FAKE, 256, 1.0, 0.5, FAKE, ws, None) == _lib.PM_EINVAL
+    assert lib.pm_gemm_symmetric(FAKE, FAKE, FAKE, FAKE, 256, 1.0, 0.5, FAKE, ws - 1, None) == _lib.PM_EWORKSPACE
+    assert lib.pm_gemm_symmetric(FAKE, FAKE, FAKE, FAKE, 256, 1.0, 0.5, FAKE + 8, ws, None) == _lib.PM_EINVAL
+
+
 def test_error_text_is_per_thread(lib):
     import threading
 
@@ -204,6 +229,16 @@ def test_workspace_sizing(lib):
     capped = ws_bytes(lib, [mat(1024, 4096)] * 3, limit=1)
     assert capped < three and capped >= one
     assert ws_bytes(lib, [mat(pdt=5)]) == 0 and "dtype" in _lib.last_error()
+
+
+def test_gram_form_workspace_sizing(lib):
+    M, N = 1024, 4096
+    std = ws_bytes(lib, [mat(M, N)])
+    hp = hparams(ns_form="gram")
+    gram = lib.pm_workspace_bytes(arr(mat(M, N)), 1, ctypes.byref(hp))
+    # the gram form keeps R, Z, RZ and two Q: three more M x M bf16 matrices
+    assert gram - std >= 3 * M * M * 2
+    assert gram - std <= 3 * M * M * 2 + (64 << 10)  # plus a larger launch table
 
 
 def test_ns_workspace_matches_step_workspace(lib):
