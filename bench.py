@@ -33,7 +33,18 @@ CONFIGS = {
     3: ("mlp_16up_16down", [(4 * S, S)] * 16 + [(S, 4 * S)] * 16),
     4: ("mmdit_block_ragged", BLOCK),
     5: ("mmdit_24_blocks", BLOCK * 24),
+    # not a BASELINE config: PAN 2's chunked QKV weights, 44 joint blocks of
+    # (2 x 3 x 4096, 4096), each orthogonalised as 192 row blocks of 128 x 4096
+    # (pan/models/transformers/pan_transformer.py:65-71, pan/optim/patch_muon.py:75-142)
+    6: ("qkv_chunks_44x192", [(6 * 4096, 4096)] * 44),
 }
+CHUNKS = {6: 192}  # row blocks per param (adjust_lr_fn = (base, 0, n))
+
+
+def unit_shapes(config: int):
+    """The matrices Newton–Schulz runs on: the params, or their row blocks."""
+    n = CHUNKS.get(config, 1)
+    return [(r // n, c) for r, c in CONFIGS[config][1] for _ in range(n)]
 
 
 def ns_flops(shape, steps=5):
@@ -241,7 +252,10 @@ def main() -> int:
     if args.workspace_gib:
         pm.WORKSPACE_LIMIT = int(args.workspace_gib * (1 << 30))
     lr = torch.tensor(0.02, dtype=torch.float32, device=device)
-    opt = torch.optim.Muon(params, lr=lr, weight_decay=0.01, momentum=0.95, adjust_lr_fn="match_rms_adamw")
+    group = {"params": params}
+    if args.config in CHUNKS:
+        group["adjust_lr_fn"] = ("match_rms_adamw", 0, CHUNKS[args.config])
+    opt = torch.optim.Muon([group], lr=lr, weight_decay=0.01, momentum=0.95, adjust_lr_fn="match_rms_adamw")
     for p, m in zip(params, moms):
         opt.state[p]["momentum_buffer"] = m
     torch.cuda.synchronize()
@@ -256,8 +270,11 @@ def main() -> int:
     _lib.timing_read()  # clear
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    host = 0.0  # time inside step() calls: host work, as the GPU work is enqueued without waiting
     for _ in range(args.steps):
+        h0 = time.perf_counter()
         opt.step()
+        host += time.perf_counter() - h0
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     recs = _lib.timing_read()
@@ -273,10 +290,11 @@ def main() -> int:
     ms_per_step = elapsed * 1e3 / args.steps
     print(f"bench: {ms_per_step:.2f} ms/step", file=sys.stderr, flush=True)
 
-    f_ns = sum(ns_flops(s) for s in shapes)
-    f_dense = sum(dense_flops(s) for s in shapes)
+    units = unit_shapes(args.config)
+    f_ns = sum(ns_flops(s) for s in units)
+    f_dense = sum(dense_flops(s) for s in units)
     # the gram form does less work than the quintic: its rate is its own executed FLOPs over time
-    f_run = f_ns if args.ns_form == "standard" else sum(gram_form_flops(s) for s in shapes)
+    f_run = f_ns if args.ns_form == "standard" else sum(gram_form_flops(s) for s in units)
     value = f_run / (ms_per_step * 1e-3) / 1e12
 
     gemm = [r for r in recs if r["kind"] in ("gram", "poly", "update", "final")]
@@ -284,7 +302,7 @@ def main() -> int:
     gemm_flops = sum(r["flops"] for r in gemm)
     achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
     stages = {}
-    for kind in ("prologue", "norm", "gram", "poly", "qinit", "update", "final"):
+    for kind in ("prologue", "norm", "gram", "poly", "qinit", "small_core", "update", "final"):
         rs = [r for r in recs if r["kind"] == kind]
         if not rs:
             continue
@@ -303,7 +321,7 @@ def main() -> int:
         from oracle.cpu_baseline import baseline
 
         print("bench: CPU baseline (stock torch Muon, host cores)", file=sys.stderr, flush=True)
-        cb = baseline(shapes, budget_s=args.cpu_budget, stock_fns=stock_fns)
+        cb = baseline(units, budget_s=args.cpu_budget, stock_fns=stock_fns)
         cpu = {
             "value": round(f_ns / (cb["step_ms"] * 1e-3) / 1e12, 4),
             "unit": "TFLOP/s",
@@ -333,8 +351,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": name,
-            "baseline_config": args.config,
-            "matrices": len(shapes),
+            "baseline_config": args.config if args.config <= 5 else None,
+            "matrices": len(units),
             "params": params_total,
             "param_dtype": "fp32" if args.config == 1 else "bf16",
             "grad_dtype": "fp32" if args.config == 1 else "bf16",
@@ -346,6 +364,7 @@ def main() -> int:
             **({"f_gram_form": f_run} if args.ns_form == "gram" else {}),
         },
         "pct_peak_step": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "host_ms_per_step": round(host * 1e3 / args.steps, 3),
         "roofline": {
             "kernel": "pm_ns_gemm_kernel",
             "bound": "mfma",

@@ -228,7 +228,10 @@ enum pm_kernel_kind {
                          Z, Q, RZ and R updates (gram form) */
   PM_K_UPDATE = 4,    /* X <- a X + B X (gram form: X <- Q X at the reset) */
   PM_K_FINAL = 5,     /* last update fused with the parameter step */
-  PM_K_QINIT = 6      /* gram form: Q = Z + a I */
+  PM_K_QINIT = 6,     /* gram form: Q = Z + a I */
+  PM_K_SMALL_CORE = 7 /* matrices with min(rows, cols) <= 128: gram and the
+                         M x M part of one iteration (standard form) or of one
+                         segment (gram form), in one launch */
 };
 
 typedef struct pm_launch_time {

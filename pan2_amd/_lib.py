@@ -10,6 +10,7 @@ import ctypes
 import os
 import threading
 
+import numpy as np
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpanmuon.so")
@@ -47,7 +48,7 @@ EXPORTS = (
     "pm_timing_read",
 )
 
-KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit")
+KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit", "small_core")
 
 
 class PmMatrix(ctypes.Structure):
@@ -66,6 +67,15 @@ class PmMatrix(ctypes.Structure):
         ("reserved", ctypes.c_int32),
         ("adj_ratio", ctypes.c_double),
     ]
+
+
+# numpy twin of PmMatrix: the row blocks of a chunked param are filled as arrays
+_PM_MATRIX_NP = np.dtype({
+    "names": [f for f, _ in PmMatrix._fields_],
+    "formats": ["u8", "u8", "u8", "i8", "i8", "i8", "i8", "i8", "i4", "i4", "i4", "i4", "f8"],
+    "offsets": [getattr(PmMatrix, f).offset for f, _ in PmMatrix._fields_],
+    "itemsize": ctypes.sizeof(PmMatrix),
+})
 
 
 class PmNsMatrix(ctypes.Structure):
@@ -231,20 +241,14 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, nesterov, ns_coefficients,
-              ns_steps, eps, workspace_limit: int = 0, ns_form: str = "standard") -> None:
-    """pm_muon_step over matching lists of 2-D device tensors (updated in place).
-
-    lr: python float, or a 1-element float tensor on the same device (read on
-    the device, no host sync).
-    """
-    lib = load()
-    n = len(params)
-    if n == 0:
-        return
+def _step_matrices(params, grads, bufs, adj_ratios, chunks):
+    """The pm_matrix array of a call: entry i of the lists becomes chunks[i]
+    equal row blocks (one matrix each, with adj_ratios[i]), addressed in place."""
+    counts = [1] * len(params) if chunks is None else [int(c) for c in chunks]
+    arr = np.zeros(sum(counts), dtype=_PM_MATRIX_NP)
     dev = params[0].device
-    mats = (PmMatrix * n)()
-    for i, (p, g, b, r) in enumerate(zip(params, grads, bufs, adj_ratios)):
+    pos = 0
+    for p, g, b, r, k in zip(params, grads, bufs, adj_ratios, counts):
         _check_matrix(p, "param")
         _check_matrix(g, "grad")
         _check_matrix(b, "momentum buffer")
@@ -252,12 +256,37 @@ def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, ne
             raise ValueError(f"param/grad/buffer shapes differ: {tuple(p.shape)}, {tuple(g.shape)}, {tuple(b.shape)}")
         if p.device != dev or g.device != dev or b.device != dev:
             raise ValueError("all tensors of one call must be on one device")
-        m = mats[i]
-        m.param, m.grad, m.momentum = p.data_ptr(), g.data_ptr(), b.data_ptr()
-        m.rows, m.cols = p.shape
-        m.param_ld, m.grad_ld, m.momentum_ld = _ld(p), _ld(g), _ld(b)
-        m.param_dtype, m.grad_dtype, m.momentum_dtype = dtype_code(p), dtype_code(g), dtype_code(b)
-        m.adj_ratio = float(r)
+        if k < 1 or p.shape[0] % k:
+            raise ValueError(f"{p.shape[0]} rows cannot be split into {k} equal row blocks")
+        rows = p.shape[0] // k
+        blk = arr[pos:pos + k]
+        idx = np.arange(k, dtype=np.uint64)
+        for field, t in (("param", p), ("grad", g), ("momentum", b)):
+            blk[field] = np.uint64(t.data_ptr()) + idx * np.uint64(rows * t.stride(0) * t.element_size())
+        blk["rows"], blk["cols"] = rows, p.shape[1]
+        blk["param_ld"], blk["grad_ld"], blk["momentum_ld"] = _ld(p), _ld(g), _ld(b)
+        blk["param_dtype"], blk["grad_dtype"], blk["momentum_dtype"] = dtype_code(p), dtype_code(g), dtype_code(b)
+        blk["adj_ratio"] = float(r)
+        pos += k
+    return arr
+
+
+def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, nesterov, ns_coefficients,
+              ns_steps, eps, workspace_limit: int = 0, ns_form: str = "standard", chunks=None) -> None:
+    """pm_muon_step over matching lists of 2-D device tensors (updated in place).
+
+    lr: python float, or a 1-element float tensor on the same device (read on
+    the device, no host sync). chunks: per entry, the number of equal row
+    blocks orthogonalised independently (None: 1 each), addressed in place
+    without building views.
+    """
+    lib = load()
+    if len(params) == 0:
+        return
+    dev = params[0].device
+    arr = _step_matrices(params, grads, bufs, adj_ratios, chunks)
+    n = len(arr)
+    mats = arr.ctypes.data_as(ctypes.POINTER(PmMatrix))
     hp, keep = make_hparams(momentum=momentum, nesterov=nesterov, ns_coefficients=ns_coefficients,
                             ns_steps=ns_steps, eps=eps, weight_decay=weight_decay,
                             workspace_limit=workspace_limit, ns_form=ns_form)
@@ -281,7 +310,7 @@ def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, ne
         ws = workspace(nbytes, dev)
         rc = lib.pm_muon_step(mats, n, ctypes.byref(hp), lr_dev, lr_host, ws.data_ptr(), nbytes, stream_of(dev))
     check(rc, "pm_muon_step")
-    del keep, lr_keep
+    del keep, lr_keep, arr
 
 
 def newton_schulz_into(pairs, *, ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7,

@@ -9,15 +9,16 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "../../include/panmuon.h"
 #include "pm_kernels.hpp"
+#include "pm_small.hpp"
 
 using namespace pm;
 
-static_assert(sizeof(BlobChunk) == 2048, "descriptor upload chunk");
 static_assert(sizeof(MatDesc) % 8 == 0, "descriptor alignment");
 // ABI layout, mirrored by the ctypes structures of pan2_amd/_lib.py
 static_assert(sizeof(pm_matrix) == 88, "pm_matrix layout");
@@ -51,16 +52,20 @@ constexpr uint64_t kDefaultWorkspaceLimit = 32ull << 30;  // 32 GiB
 size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// Shape plan of one matrix: orientation and padded extents.
+// Shape plan of one matrix: orientation and padded extents. A matrix whose
+// short side is at most 128 is "small": padded to 128 and run by the
+// small-matrix kernels (pm_small.hpp) instead of the grouped GEMM engine.
 struct Plan {
   int32_t rows, cols, trans, M, N, Mp, Np;
+  bool small;
   size_t ws;  // workspace bytes of this matrix
   double flops;
 };
 
 // Square Mp x Mp work matrices per matrix: A and B (standard form) or R, Z,
-// RZ and two Q (gram form).
-int square_bufs(int form) { return form == NS_GRAM ? 5 : 2; }
+// RZ and two Q (gram form); a small matrix keeps its work matrices in LDS and
+// needs one, the S its core launch hands to its apply launch.
+int square_bufs(int form, bool small) { return small ? 1 : form == NS_GRAM ? 5 : 2; }
 
 Plan make_plan(int64_t rows, int64_t cols, int form) {
   Plan p{};
@@ -69,12 +74,13 @@ Plan make_plan(int64_t rows, int64_t cols, int form) {
   p.trans = rows > cols;
   p.M = (int32_t)std::min(rows, cols);
   p.N = (int32_t)std::max(rows, cols);
-  p.Mp = (int32_t)round_up(p.M, kTile);
+  p.small = p.M <= kSm;
+  p.Mp = p.small ? kSm : (int32_t)round_up(p.M, kTile);
   p.Np = (int32_t)round_up(p.N, kTile);
   const size_t x = align_up((size_t)p.Mp * p.Np * 2);
   const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
   const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);
-  p.ws = 4 * x + (size_t)square_bufs(form) * a + part + kAlign;
+  p.ws = 4 * x + (size_t)square_bufs(form, p.small) * a + part + kAlign;
   const double M = p.M, N = p.N;
   p.flops = M * (M + 1) * N + M * M * (M + 1) + 2 * M * M * N;
   return p;
@@ -92,13 +98,15 @@ int gemm_launches(const pm_hparams* hp) {
 }
 
 // Descriptor table layout:
-//   descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1] | queues[launches][kXcds]
+//   descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1] | queues[launches][kXcds] | coeffs
 // The queue counters are uploaded as zeros with the rest of the table, so
-// every GEMM launch starts with empty counters without a memset.
-size_t table_bytes(int n, int launches) {
-  return align_up((size_t)n * sizeof(MatDesc)) + 3 * align_up((size_t)(n + 1) * 4) +
-         align_up((size_t)launches * kXcds * 4);
-}
+// every GEMM launch starts with empty counters without a memset. coeffs holds
+// the (a, b, c) of every iteration, which the small-matrix core launch reads.
+constexpr int kMaxSteps = 99;
+constexpr size_t kCoeffBytes = (3 * kMaxSteps * 4 + kAlign - 1) / kAlign * kAlign;
+size_t queue_offset(int n) { return align_up((size_t)n * sizeof(MatDesc)) + 3 * align_up((size_t)(n + 1) * 4); }
+size_t coeff_offset(int n, int launches) { return queue_offset(n) + align_up((size_t)launches * kXcds * 4); }
+size_t table_bytes(int n, int launches) { return coeff_offset(n, launches) + kCoeffBytes; }
 
 // Persistent GEMM grid: one block per CU (the kernel's LDS allows no more),
 // never more blocks than tiles.
@@ -118,8 +126,8 @@ bool valid_dtype(int32_t dt) { return dt == PM_DTYPE_F32 || dt == PM_DTYPE_BF16;
 
 int check_hparams(const pm_hparams* hp) {
   if (!hp) return fail(PM_EINVAL, "hparams is NULL");
-  if (hp->ns_steps < 1 || hp->ns_steps >= 100)
-    return fail(PM_EUNSUPPORTED, "ns_steps must be in [1, 99], got %d", hp->ns_steps);
+  if (hp->ns_steps < 1 || hp->ns_steps > kMaxSteps)
+    return fail(PM_EUNSUPPORTED, "ns_steps must be in [1, %d], got %d", kMaxSteps, hp->ns_steps);
   if (hp->ns_form != PM_NS_STANDARD && hp->ns_form != PM_NS_GRAM)
     return fail(PM_EINVAL, "ns_form must be PM_NS_STANDARD or PM_NS_GRAM, got %d", hp->ns_form);
   if (!(hp->eps >= 0.0f)) return fail(PM_EINVAL, "eps must be >= 0");
@@ -145,7 +153,7 @@ int32_t sym_tiles(const Plan& p) {
   const int32_t nt = p.Mp / kTile;
   return nt * (nt + 1) / 2;
 }
-int32_t full_tiles(const Plan& p) { return (p.Mp / kTile) * (p.Np / kTile); }
+int32_t full_tiles(const Plan& p) { return p.small ? p.Np / kTile : (p.Mp / kTile) * (p.Np / kTile); }
 
 // One matrix of a call, whatever the entry point.
 struct Item {
@@ -153,21 +161,67 @@ struct Item {
   MatDesc desc;
 };
 
+// Descriptor uploads go through pinned staging buffers: the host table is
+// copied into one, and an asynchronous copy on the caller's stream moves it
+// to the workspace, so the host never waits for the stream. A buffer is
+// reused once the event recorded after its copy has completed; the pool
+// grows while every buffer is still in flight (a call queued far behind the
+// GPU), up to kMaxStaging buffers per device, after which the oldest is
+// waited for.
+struct Staging {
+  int device;
+  void* host;
+  size_t bytes;
+  hipEvent_t done;
+};
+constexpr size_t kMaxStaging = 64;
+std::mutex g_stage_mu;
+std::vector<Staging> g_stage;
+
 int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
-  const uint32_t* w = (const uint32_t*)src;
-  size_t nwords = bytes / 4;
-  uint32_t* d = (uint32_t*)dst;
-  BlobChunk chunk;
-  while (nwords) {
-    const int k = (int)std::min<size_t>(nwords, 512);
-    std::memcpy(chunk.w, w, (size_t)k * 4);
-    hipLaunchKernelGGL(pm_upload_kernel, dim3(1), dim3(256), 0, stream, chunk, d, k);
-    w += k;
-    d += k;
-    nwords -= k;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_stage_mu);
+  Staging* s = nullptr;
+  size_t mine = 0, oldest = SIZE_MAX;
+  for (size_t i = 0; i < g_stage.size(); ++i) {
+    Staging& c = g_stage[i];
+    if (c.device != dev) continue;
+    ++mine;
+    if (oldest == SIZE_MAX) oldest = i;
+    if (hipEventQuery(c.done) != hipSuccess) continue;  // its copy is still queued
+    if (!s || c.bytes > s->bytes) s = &c;              // a free buffer, the largest
   }
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? PM_OK : hip_fail(e, "descriptor upload launch");
+  if (!s && mine >= kMaxStaging) {
+    s = &g_stage[oldest];
+    e = hipEventSynchronize(s->done);
+    if (e != hipSuccess) return hip_fail(e, "staging event");
+  }
+  if (!s) {
+    Staging c{dev, nullptr, 0, nullptr};
+    e = hipEventCreateWithFlags(&c.done, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "staging event create");
+    g_stage.push_back(c);
+    s = &g_stage.back();
+  }
+  if (s->bytes < bytes) {
+    if (s->host) {
+      e = hipHostFree(s->host);  // its copy has completed
+      s->host = nullptr;
+      s->bytes = 0;
+      if (e != hipSuccess) return hip_fail(e, "staging free");
+    }
+    const size_t want = std::max<size_t>(align_up(bytes, 1 << 16), 1 << 16);
+    e = hipHostMalloc(&s->host, want, hipHostMallocDefault);
+    if (e != hipSuccess) return hip_fail(e, "staging allocation");
+    s->bytes = want;
+  }
+  std::memcpy(s->host, src, bytes);
+  e = hipMemcpyAsync(dst, s->host, bytes, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_fail(e, "descriptor upload");
+  e = hipEventRecord(s->done, stream);
+  return e == hipSuccess ? PM_OK : hip_fail(e, "staging event record");
 }
 
 struct Coeff {
@@ -286,6 +340,31 @@ struct Launcher {
     timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
     return check("Newton-Schulz update launch");
   }
+  // small matrices: R = X Xᵀ and the M x M part of `steps` iterations from it0
+  // (steps == 0: the standard form's B) into S[0]
+  const float* coeffs = nullptr;  // device (a, b, c) per iteration
+  int small_core(int cur, bool first, int it0, int steps, int it) {
+    const SmallCoreArgs a{ga.descs, coeffs, it0, steps, cur, first, 0, 0};
+    hipLaunchKernelGGL(pm_small_core_kernel, dim3(count), dim3(kGemmThreads), 0, stream, a);
+    const int products = steps == 0 ? 1 : 4 * steps - 3;
+    timing_mark(stream, PM_K_SMALL_CORE, group, it, count, f_gram + products * f_sym, 0.0);
+    return check("small-matrix core launch");
+  }
+  // small matrices: X' = s·(a·X + S[0]·X), or (last) the param step
+  int small_apply(float coef_a, int cur, bool first, bool last, int it) {
+    GemmArgs a = ga;
+    a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = 0; a.a = coef_a; a.cur = cur; a.first = first;
+    a.prefix = full; a.total = full_total;
+    const dim3 grid(full_total), block(kSmApplyThreads);
+    if (last && final_f32)
+      hipLaunchKernelGGL((pm_small_apply_kernel<ST_FINAL, DT_F32>), grid, block, 0, stream, a);
+    else if (last)
+      hipLaunchKernelGGL((pm_small_apply_kernel<ST_FINAL, DT_BF16>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((pm_small_apply_kernel<ST_UPDATE, DT_BF16>), grid, block, 0, stream, a);
+    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
+    return check("small-matrix apply launch");
+  }
   int qinit(int sz, int sq, float coef_a, int max_mp, int it) {
     for (int first = 0; first < count; first += 65535)  // gridDim.y limit
       hipLaunchKernelGGL(pm_qinit_kernel, dim3(max_mp / kProTile, std::min(count - first, 65535)), dim3(kThreads), 0,
@@ -365,7 +444,34 @@ int run_gram(Launcher& L, const pm_hparams* hp, int max_mp) {
   return rc;
 }
 
-// Runs one group: items[0, count) share the workspace `ws`.
+// Small matrices (pm_small.hpp). Standard form: per iteration one core launch
+// (R and B) and one apply. Gram form: one core launch per segment (R, then the
+// segment's Z, Q and R updates) and one apply of its Q, the second segment
+// starting at the reset iteration on the applied X.
+int run_small(Launcher& L, const pm_hparams* hp) {
+  const int steps = hp->ns_steps;
+  if (hp->ns_form != NS_GRAM) {
+    const Coeffs co{hp};
+    for (int it = 0; it < steps; ++it) {
+      int rc = L.small_core(it & 1, it == 0, it, 0, it);
+      if (!rc) rc = L.small_apply(co.at(it).a, it & 1, it == 0, it + 1 == steps, it);
+      if (rc) return rc;
+    }
+    return PM_OK;
+  }
+  const int reset = gram_reset(steps);
+  const int seg1 = reset > 0 ? reset : steps;
+  int rc = L.small_core(0, true, 0, seg1, 0);
+  if (!rc) rc = L.small_apply(0.0f, 0, true, seg1 == steps, seg1 - 1);
+  if (!rc && seg1 < steps) {
+    rc = L.small_core(1, false, seg1, steps - seg1, seg1);
+    if (!rc) rc = L.small_apply(0.0f, 1, false, true, steps - 1);
+  }
+  return rc;
+}
+
+// Runs one group: items[0, count) share the workspace `ws` and are all small
+// or all not.
 int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
               double lr_host, char* ws, hipStream_t stream) {
   const int form = hp->ns_form;
@@ -378,6 +484,14 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   int32_t* sym = (int32_t*)((char*)pro + align_up((size_t)(count + 1) * 4));
   int32_t* full = (int32_t*)((char*)sym + align_up((size_t)(count + 1) * 4));
   const int32_t* queues = (const int32_t*)((char*)full + align_up((size_t)(count + 1) * 4));  // zeros
+  float* coeffs = (float*)(host.data() + coeff_offset(count, gemm_launches(hp)));
+  const Coeffs co{hp};
+  for (int it = 0; it < hp->ns_steps; ++it) {
+    const Coeff k = co.at(it);
+    coeffs[3 * it] = k.a;
+    coeffs[3 * it + 1] = k.b;
+    coeffs[3 * it + 2] = k.c;
+  }
   pro[0] = sym[0] = full[0] = 0;
   int max_mp = 0;
   for (int i = 0; i < count; ++i) {
@@ -393,8 +507,8 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     d.XT[0] = (uint16_t*)cursor; cursor += x;
     d.XT[1] = (uint16_t*)cursor; cursor += x;
     for (int b = 0; b < kSquareBufs; ++b) {
-      d.S[b] = b < square_bufs(form) ? (uint16_t*)cursor : nullptr;
-      if (b < square_bufs(form)) cursor += a;
+      d.S[b] = b < square_bufs(form, p.small) ? (uint16_t*)cursor : nullptr;
+      if (b < square_bufs(form, p.small)) cursor += a;
     }
     d.partials = (float*)cursor; cursor += align_up((size_t)pro_tiles(p) * 4);
     d.scales = (float*)cursor; cursor += kAlign;
@@ -465,6 +579,8 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   L.f_gram = f_gram;
   L.f_sym = f_sym;
   L.f_upd = f_upd;
+  L.coeffs = (const float*)(ws + ((char*)coeffs - host.data()));
+  if (items[0].plan.small) return run_small(L, hp);
   return form == NS_GRAM ? run_gram(L, hp, max_mp) : run_standard(L, hp);
 }
 
@@ -475,9 +591,11 @@ int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const floa
   if (items.empty()) return PM_OK;
   if (!workspace) return fail(PM_EINVAL, "workspace is NULL");
   if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
-  // params of one dtype together (one FINAL epilogue per launch), then longest tiles first
+  // params of one dtype together (one FINAL epilogue per launch), small
+  // matrices apart from the rest (other kernels), then longest tiles first
   std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) {
     if (x.desc.p_dt != y.desc.p_dt) return x.desc.p_dt < y.desc.p_dt;
+    if (x.plan.small != y.plan.small) return y.plan.small;
     return x.plan.Np != y.plan.Np ? x.plan.Np > y.plan.Np : x.plan.Mp > y.plan.Mp;
   });
   size_t i = 0;
@@ -486,6 +604,7 @@ int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const floa
     size_t j = i, need = 0;
     while (j < items.size()) {
       if (items[j].desc.p_dt != items[i].desc.p_dt) break;  // one param dtype per group
+      if (items[j].plan.small != items[i].plan.small) break;  // one kind of kernels per group
       const size_t next = need + items[j].plan.ws;
       if (table_bytes((int)(j - i + 1), gemm_launches(hp)) + next > ws_bytes) break;
       need = next;
@@ -700,7 +819,7 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   d->rows = (int32_t)rows;
   d->cols = (int32_t)cols;
   int32_t* sym = (int32_t*)(host.data() + align_up(sizeof(MatDesc)) + align_up(8));
-  const size_t queues_off = align_up(sizeof(MatDesc)) + 3 * align_up(8);  // one launch's counters, zeros
+  const size_t queues_off = queue_offset(1);  // one launch's counters, zeros
   const int32_t nt = (int32_t)(rows / kTile);
   sym[0] = 0;
   sym[1] = nt * (nt + 1) / 2;
@@ -743,7 +862,7 @@ int pm_gemm_symmetric(const void* left, const void* right, const void* addend, v
   d->Mp = d->M = d->Np = d->N = (int32_t)m;
   d->rows = d->cols = (int32_t)m;
   int32_t* sym = (int32_t*)(host.data() + align_up(sizeof(MatDesc)) + align_up(8));
-  const size_t queues_off = align_up(sizeof(MatDesc)) + 3 * align_up(8);  // one launch's counters, zeros
+  const size_t queues_off = queue_offset(1);  // one launch's counters, zeros
   const int32_t nt = (int32_t)(m / kTile);
   sym[0] = 0;
   sym[1] = nt * (nt + 1) / 2;

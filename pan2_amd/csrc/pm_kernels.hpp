@@ -976,12 +976,4 @@ __global__ __launch_bounds__(kThreads) void pm_step_kernel(void* param, int32_t 
   }
 }
 
-// Copies a by-value chunk of the descriptor table into the workspace.
-struct BlobChunk {
-  uint32_t w[512];
-};
-__global__ void pm_upload_kernel(BlobChunk chunk, uint32_t* dst, int nwords) {
-  for (int i = threadIdx.x; i < nwords; i += blockDim.x) dst[i] = chunk.w[i];
-}
-
 }  // namespace pm

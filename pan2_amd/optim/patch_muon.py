@@ -89,7 +89,7 @@ def _single_tensor_muon(
     if not params:
         return
 
-    p_list, g_list, b_list, ratios = [], [], [], []
+    p_list, g_list, b_list, ratios, counts = [], [], [], [], []
     for param, grad, buf in zip(params, grads, muon_momentum_bufs):
         _require_matrix(grad)
         assert nesterov
@@ -105,20 +105,16 @@ def _single_tensor_muon(
             assert R % total_chunks == 0, "# rows must be divisible by # local chunks (chunks must be same-shape)"
         if not param.is_cuda:
             raise RuntimeError("pan2_amd Muon runs on HIP device tensors only; got a CPU parameter")
+        p_list.append(param)
+        g_list.append(grad)
+        b_list.append(buf)
         if chunk_dim == 0:
-            rows = R // total_chunks
-            ratio = _adjust_ratio(base_adjust_lr_fn, (rows, N))
-            for k in range(total_chunks):
-                sl = slice(k * rows, (k + 1) * rows)
-                p_list.append(param[sl])
-                g_list.append(grad[sl])
-                b_list.append(buf[sl])
-                ratios.append(ratio)
+            # row blocks param[k*rows:(k+1)*rows], addressed in place by the library
+            ratios.append(_adjust_ratio(base_adjust_lr_fn, (R // total_chunks, N)))
+            counts.append(total_chunks)
         else:
-            p_list.append(param)
-            g_list.append(grad)
-            b_list.append(buf)
             ratios.append(_adjust_ratio(base_adjust_lr_fn, param.shape))
+            counts.append(1)
 
     by_device: dict[torch.device, list[int]] = {}
     for i, p in enumerate(p_list):
@@ -126,7 +122,7 @@ def _single_tensor_muon(
     for dev, idx in by_device.items():
         _lib.muon_step(
             [p_list[i] for i in idx], [g_list[i] for i in idx], [b_list[i] for i in idx],
-            [ratios[i] for i in idx],
+            [ratios[i] for i in idx], chunks=[counts[i] for i in idx],
             lr=lr, weight_decay=weight_decay, momentum=momentum, nesterov=nesterov,
             ns_coefficients=ns_coefficients, ns_steps=ns_steps, eps=eps,
             workspace_limit=WORKSPACE_LIMIT, ns_form=NS_FORM,

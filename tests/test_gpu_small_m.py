@@ -1,0 +1,196 @@
+"""GPU parity of the small-matrix path (min(rows, cols) <= 128: PAN 2's chunked
+QKV row blocks, [B, 128, N], pan/optim/patch_muon.py:75-142 and
+pan/optim/muon_triton.py:234-345), through the C ABI.
+
+Three kinds of checks:
+- against the oracle: relative Frobenius error vs the fp64 standard quintic
+  <= 2e-2 (standard form), or the gram-form gate of test_gpu_gram_form (max(2e-2,
+  1.25 x the bf16 gram-form restatement's own error));
+- against the grouped GEMM engine, bit for bit: a small matrix padded with
+  zero rows (or columns) to a short side of 256 runs through the engine and
+  must give the same bf16 output on the real rows. The inputs are multiples of
+  1/4 in [-1, 1], so the Frobenius norm is exact in fp32 whatever the
+  summation order, and every later product is the same MFMA over the same k
+  order in both paths;
+- determinism and grouping: mixed small / large calls equal per-matrix calls.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import muon_ref
+from pan2_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def seeded(shape, seed, std=1.0):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float32) * std
+
+
+def quarters(shape, seed):
+    """Entries in {0, ±1/4, ±1/2, ±3/4, ±1}: exact in bf16, squares exact in fp32 sums."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randint(-4, 5, shape, generator=g).float() / 4
+
+
+def rel_fro(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def ns(x, **kw):
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=DEV)
+    _lib.newton_schulz_into([(x.to(DEV), out)], **kw)
+    return out
+
+
+SMALL_SHAPES = [(128, 4096), (4096, 128), (128, 128), (100, 1000), (1000, 100), (128, 300), (17, 5), (1, 260)]
+
+
+@pytest.mark.parametrize("rows,cols", SMALL_SHAPES)
+def test_small_standard_vs_fp64(rows, cols):
+    print(f"small standard ns {rows}x{cols}", flush=True)
+    g = seeded((rows, cols), 808 + rows * 3 + cols)
+    o = ns(g).float().cpu().numpy()
+    ref = muon_ref.ns_standard(g.numpy(), precision="fp64")
+    oracle = muon_ref.ns_standard(g.numpy(), precision="bf16")
+    assert rel_fro(o, ref) <= 2e-2
+    assert rel_fro(o, oracle) <= 2e-2
+
+
+@pytest.mark.parametrize("rows,cols", SMALL_SHAPES)
+def test_small_gram_form_vs_fp64(rows, cols):
+    print(f"small gram-form ns {rows}x{cols}", flush=True)
+    g = seeded((rows, cols), 909 + rows * 5 + cols)
+    o = ns(g, ns_form="gram").float().cpu().numpy()
+    ref = muon_ref.ns_standard(g.numpy(), precision="fp64")
+    oracle = muon_ref.ns_gram(g.numpy(), precision="bf16")
+    gate = max(2e-2, 1.25 * rel_fro(oracle, ref))
+    assert rel_fro(o, ref) <= gate
+    assert rel_fro(o, oracle) <= np.sqrt(2) * gate
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+@pytest.mark.parametrize("rows,cols,transpose", [(128, 2048, False), (100, 1000, False), (128, 768, True),
+                                                 (64, 300, True)])
+def test_small_equals_engine_on_padded_matrix(ns_form, rows, cols, transpose):
+    """The engine on [X; 0] (short side padded to 256 with zeros) gives X's
+    rows bit for bit: the small kernels are the engine's arithmetic on 128."""
+    print(f"small vs engine {ns_form} {rows}x{cols} transpose={transpose}", flush=True)
+    x = quarters((rows, cols), 31 + rows + cols)
+    padded = torch.zeros((256, cols))
+    padded[:rows] = x
+    if transpose:
+        x, padded = x.T.contiguous(), padded.T.contiguous()
+    small = ns(x, ns_form=ns_form)
+    big = ns(padded, ns_form=ns_form)
+    big = big[:, :rows] if transpose else big[:rows]
+    assert torch.count_nonzero(small).item() > 0
+    assert torch.equal(small, big)
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+@pytest.mark.parametrize("steps", [1, 2, 3, 5])
+def test_small_step_counts(ns_form, steps):
+    print(f"small {ns_form} steps={steps}", flush=True)
+    g = seeded((128, 1536), 70 + steps)
+    o = ns(g, ns_steps=steps, ns_form=ns_form).float().cpu().numpy()
+    ref = muon_ref.ns_standard(g.numpy(), precision="fp64", ns_steps=steps)
+    if ns_form == "standard":
+        gate = 2e-2
+    else:
+        gate = max(2e-2, 1.25 * rel_fro(muon_ref.ns_gram(g.numpy(), precision="bf16", ns_steps=steps), ref))
+    assert rel_fro(o, ref) <= gate
+    # equal to the engine on the zero-padded matrix, at every step count
+    x = quarters((128, 1536), 170 + steps)
+    padded = torch.zeros((256, 1536))
+    padded[:128] = x
+    assert torch.equal(ns(x, ns_steps=steps, ns_form=ns_form), ns(padded, ns_steps=steps, ns_form=ns_form)[:128])
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+def test_small_per_step_coefficients(ns_form):
+    coeffs = [(3.4445, -4.7750, 2.0315), (3.0, -3.2, 1.2), (3.4445, -4.7750, 2.0315), (2.5, -2.0, 0.6),
+              (1.9, -1.4, 0.5)]
+    g = seeded((128, 2048), 2025)
+    o = ns(g, ns_coefficients=coeffs, ns_form=ns_form).float().cpu().numpy()
+    ref = muon_ref.ns_standard(g.numpy(), precision="fp64", ns_coefficients=coeffs)
+    oracle_fn = muon_ref.ns_gram if ns_form == "gram" else muon_ref.ns_standard
+    oracle = oracle_fn(g.numpy(), precision="bf16", ns_coefficients=coeffs)
+    gate = max(2e-2, 1.25 * rel_fro(oracle, ref))
+    assert rel_fro(o, ref) <= gate
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+def test_small_and_large_grouped_equal_single_and_deterministic(ns_form):
+    shapes = [(128, 1024), (512, 1024), (64, 200), (1024, 96), (300, 700), (128, 128)]
+    gs = [seeded(s, 900 + i).to(DEV) for i, s in enumerate(shapes)]
+    outs = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shapes]
+    _lib.newton_schulz_into(list(zip(gs, outs)), ns_form=ns_form)
+    again = [torch.empty_like(o) for o in outs]
+    _lib.newton_schulz_into(list(zip(gs, again)), ns_form=ns_form)
+    capped = [torch.empty_like(o) for o in outs]
+    _lib.newton_schulz_into(list(zip(gs, capped)), ns_form=ns_form, workspace_limit=1)
+    for g, o, a, c in zip(gs, outs, again, capped):
+        single = torch.empty_like(o)
+        _lib.newton_schulz_into([(g, single)], ns_form=ns_form)
+        assert torch.equal(o, single)
+        assert torch.equal(o, a)
+        assert torch.equal(o, c)
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+def test_small_zero_input(ns_form):
+    g = torch.zeros((128, 1024), device=DEV)
+    out = torch.full((128, 1024), 7.0, dtype=torch.bfloat16, device=DEV)
+    _lib.newton_schulz_into([(g, out)], ns_form=ns_form)
+    assert torch.count_nonzero(out).item() == 0
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+def test_chunked_qkv_muon_step(ns_form, pdt):
+    """PAN 2's chunked QKV group (adjust_lr_fn = (base, 0, n_chunks)): each
+    128-row block is orthogonalised on its own, the lr adjusted with the chunk
+    shape; momentum is bit-exact, every chunk's update within the gate."""
+    import pan2_amd.optim.patch_muon as pm
+
+    n_chunks, rows, cols = 12, 128, 512
+    lr, wd = 0.02, 0.01
+    p0 = seeded((n_chunks * rows, cols), 5, 0.02).to(pdt)
+    g0 = seeded((n_chunks * rows, cols), 6, 1e-3).to(pdt)
+    b0 = seeded((n_chunks * rows, cols), 7, 1e-3)
+    p = torch.nn.Parameter(p0.to(DEV).clone())
+    p.grad = g0.to(DEV)
+    opt = torch.optim.Muon([{"params": [p], "adjust_lr_fn": ("match_rms_adamw", 0, n_chunks)}],
+                           lr=torch.tensor(lr, device=DEV), weight_decay=wd, adjust_lr_fn="match_rms_adamw")
+    opt.state[p]["momentum_buffer"] = b0.to(DEV).clone()
+    saved = pm.NS_FORM
+    pm.patch_muon(ns_form=ns_form)
+    try:
+        opt.step()
+    finally:
+        pm.NS_FORM = saved
+    torch.cuda.synchronize()
+    got = p.detach().float().cpu().numpy().astype(np.float64)
+    buf = opt.state[p]["momentum_buffer"].cpu().numpy()
+    ratio = muon_ref.adjust_lr_ratio("match_rms_adamw", (rows, cols))
+    pf, gf = p0.float().numpy(), g0.float().numpy()
+    for k in range(n_chunks):
+        sl = slice(k * rows, (k + 1) * rows)
+        _, ref_b, ref_o = muon_ref.muon_step(pf[sl], gf[sl], b0.numpy()[sl], lr=lr, weight_decay=wd,
+                                             ns_precision="fp64")
+        assert np.array_equal(buf[sl], ref_b), "momentum must be bit-exact"
+        o_got = (pf[sl].astype(np.float64) * (1 - lr * wd) - got[sl]) / (lr * ratio)
+        tol = 2e-2
+        if pdt == torch.bfloat16:
+            # the new bf16 param is rounded once (at most half an ulp of p per element), which
+            # moves the recovered update by at most that over lr * ratio
+            half_ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(got[sl]), 1e-30))) - 8)
+            tol += np.linalg.norm(half_ulp) / (lr * ratio * np.linalg.norm(ref_o))
+        assert rel_fro(o_got, ref_o) <= tol, k
