@@ -153,7 +153,9 @@ int32_t sym_tiles(const Plan& p) {
   const int32_t nt = p.Mp / kTile;
   return nt * (nt + 1) / 2;
 }
-int32_t full_tiles(const Plan& p) { return p.small ? p.Np / kTile : (p.Mp / kTile) * (p.Np / kTile); }
+int32_t full_tiles(const Plan& p) {
+  return p.small ? (p.Np + kSmApplyCols - 1) / kSmApplyCols : (p.Mp / kTile) * (p.Np / kTile);
+}
 
 // One matrix of a call, whatever the entry point.
 struct Item {

@@ -12,7 +12,7 @@
 //                            _gram_newtonschulz_local (pan/optim/patch_muon.py:
 //                            320-331): Z = c R² + b R; Q = a I + Z, then
 //                            Q Z + a Q; R <- Z (R Z + a R) + a (R Z + a R); S = Q
-//   pm_small_apply_kernel  X' = s·(a·X + S X) over 128 x 256 tiles through the
+//   pm_small_apply_kernel  X' = s·(a·X + S X) over 128-row tiles through the
 //                          grouped engine's UPDATE / FINAL epilogues (X' and
 //                          X'ᵀ, or the fused parameter step)
 //
@@ -32,8 +32,14 @@ constexpr int kSm = 128;              // padded short side of a small matrix
 constexpr int kSmRow = kSm * 2;       // 256 B: a row of a 128 x 128 bf16 matrix, or 128 k values
 constexpr int kSmMat = kSm * kSmRow;  // 32 KiB: one 128 x 128 bf16 matrix
 constexpr int kSmUnit = kSm * 128;    // 16 KiB: 128 rows x 64 k values, one gram unit
-constexpr int kSmRing = 8;            // gram units in LDS (the whole 128 KiB)
-constexpr int kSmApplyThreads = 256;  // apply blocks: four waves of 128 x 64
+constexpr int kSmRing = 8;            // gram units in LDS: 7 in flight while one is read
+#ifndef PM_SMALL_APPLY_WAVES
+#define PM_SMALL_APPLY_WAVES 8
+#endif
+constexpr int kSmApplyWaves = PM_SMALL_APPLY_WAVES;  // apply blocks: waves of 128 x 64
+constexpr int kSmApplyThreads = 64 * kSmApplyWaves;
+constexpr int kSmApplyCols = 64 * kSmApplyWaves;     // columns of X per apply tile
+static_assert(kSmApplyWaves == 2 || kSmApplyWaves == 4 || kSmApplyWaves == 8, "apply tile width");
 
 struct SmallCoreArgs {
   const MatDesc* descs;
@@ -46,11 +52,34 @@ struct SmallCoreArgs {
   int32_t pad_;
 };
 
-// 128 x 128 bf16 matrices in LDS: row r is 256 B, and chunk c (16 B, columns
+// A buffer resource over [base, base + bytes). Descriptor fields reach
+// registers through vector loads (the compiler cannot prove the table
+// unclobbered), and a resource built from them would stay in VGPRs, turning
+// every buffer load into a waterfall loop; the values are uniform, so
+// readfirstlane moves them to SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const uint16_t* base, uint32_t bytes) {
+  const uint64_t v = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return panel_rsrc((const uint16_t*)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
+
+// A 128 x 128 bf16 matrix in LDS, rows 0..63 in h[0] and 64..127 in h[1]
+// (two 16 KiB gram-ring slots). Row r is 256 B and chunk c (16 B, columns
 // 8c .. 8c+7) of row r is stored at chunk c ^ (r & 15), so the 16 rows of an
-// MFMA operand read of one chunk hit 16 different bank groups.
-__device__ __forceinline__ int sm_off(int r, int c16) { return r * kSmRow + ((c16 ^ (r & 15)) << 4); }
-__device__ __forceinline__ int sm_elem(int r, int q) { return sm_off(r, q >> 3) + (q & 7) * 2; }
+// MFMA operand read of one chunk hit 16 different bank groups. Every access
+// below names its half from wave-uniform values.
+struct SmMat {
+  char* h[2];
+};
+// chunk c16 of row (64·half + rr)
+__device__ __forceinline__ char* sm_at(const SmMat& m, int half, int rr, int c16) {
+  return m.h[half] + rr * kSmRow + ((c16 ^ (rr & 15)) << 4);
+}
+// element (64·half + rr, q)
+__device__ __forceinline__ uint16_t* sm_el(const SmMat& m, int half, int rr, int q) {
+  return (uint16_t*)(sm_at(m, half, rr, q >> 3) + (q & 7) * 2);
+}
 
 __device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -69,29 +98,30 @@ __device__ __forceinline__ void store_lower4(uint16_t* dst, u16x4 v, int p0, int
     if (p0 + e < q) dst[e] = v[e];
 }
 
-// Finishes a 128 x 128 product of 8 waves, wave w owning rows r0 .. r0+63 and
-// columns c0 .. c0+31 (acc[i][j]: rows r0 + 16i + 4(lane/16) + 0..3, column
-// c0 + 16j + lane%16): C = alpha·acc + beta·D, rounded to bf16, elements on
-// and above the diagonal stored at (p, q) and (q, p), so C is exactly
-// symmetric. D must be symmetric (it is read through its transpose). C may be
-// an operand of the product: every wave has read its operands before the
-// first store.
-__device__ __forceinline__ void sm_finish(char* lds, const f32x4 (&acc)[4][2], int D, int C, float alpha, float beta,
-                                          int r0, int c0, int lane) {
+// Finishes a 128 x 128 product of 8 waves, wave w owning rows r0 .. r0+63
+// (r0 = 64·(w/4)) and columns c0 .. c0+31 (c0 = 32·(w%4)); acc[i][j] holds
+// rows r0 + 16i + 4(lane/16) + 0..3 of column c0 + 16j + lane%16.
+// C = alpha·acc + beta·D, rounded to bf16; elements on and above the diagonal
+// are stored at (p, q) and (q, p), so C is exactly symmetric. D must be
+// symmetric (it is read through its transpose). C may be an operand of the
+// product: every wave has read its operands before the first store.
+__device__ __forceinline__ void sm_finish(const f32x4 (&acc)[4][2], const SmMat& D, const SmMat& C, float alpha,
+                                          float beta, int r0, int c0, int lane) {
 #pragma clang fp contract(off)
   const int g = lane >> 4;
+  const int rh = r0 >> 6, ch = c0 >> 6, cr = c0 & 63;  // halves and row-in-half base of the wave
   u16x4 o[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int p0 = r0 + 16 * i + 4 * g, q = c0 + 16 * j + (lane & 15);
+      const int p0 = r0 + 16 * i + 4 * g;
       u16x4 dv = (u16x4){0, 0, 0, 0};
-      if (beta != 0.0f) dv = *(const u16x4*)(lds + D + sm_elem(q, p0));  // D[p0..p0+3][q]
+      if (beta != 0.0f) dv = *(const u16x4*)sm_el(D, ch, cr + 16 * j + (lane & 15), p0);  // D[p0..p0+3][q]
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[i][j][r] = f2bf(alpha * acc[i][j][r] + beta * bf2f(dv[r]));
     }
-  __syncthreads();  // every wave has read L, R and D
+  __syncthreads();  // every wave has read its operands and D
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -99,17 +129,17 @@ __device__ __forceinline__ void sm_finish(char* lds, const f32x4 (&acc)[4][2], i
       const int p0 = r0 + 16 * i + 4 * g, q = c0 + 16 * j + (lane & 15);
       // row p0 + lane%4, columns q&~3 .. +3 (quad_transpose), on and above the diagonal
       const u16x4 t = quad_transpose(o[i][j], lane);
-      store_upper4((uint16_t*)(lds + C + sm_elem(p0 + (lane & 3), q & ~3)), t, q & ~3, p0 + (lane & 3));
+      store_upper4(sm_el(C, rh, 16 * i + 4 * g + (lane & 3), q & ~3), t, q & ~3, p0 + (lane & 3));
       // the mirror: row q, columns p0 .. p0+3, strictly below the diagonal
-      store_lower4((uint16_t*)(lds + C + sm_elem(q, p0)), o[i][j], p0, q);
+      store_lower4(sm_el(C, ch, cr + 16 * j + (lane & 15), p0), o[i][j], p0, q);
     }
   __syncthreads();
 }
 
-// C = alpha·L·Rᵀ + beta·D on 128 x 128 LDS matrices (K = 128); L, R and D
-// are offsets into lds. Every matrix here is symmetric, so L Rᵀ = L R.
-__device__ __forceinline__ void sm_product(char* lds, int L, int R, int D, int C, float alpha, float beta,
-                                           int wave, int lane) {
+// C = alpha·L·Rᵀ + beta·D on 128 x 128 LDS matrices (K = 128). Every matrix
+// here is symmetric, so L Rᵀ = L R.
+__device__ __forceinline__ void sm_product(const SmMat& L, const SmMat& R, const SmMat& D, const SmMat& C, float alpha,
+                                           float beta, int wave, int lane) {
   const int r0 = (wave >> 2) * 64, c0 = (wave & 3) * 32;
   const int r16 = lane & 15, g = lane >> 4;
   f32x4 acc[4][2];
@@ -121,24 +151,24 @@ __device__ __forceinline__ void sm_product(char* lds, int L, int R, int D, int C
   for (int s = 0; s < 4; ++s) {  // k = 32s .. 32s+31: logical chunks 4s .. 4s+3
     bf16x8 a[4], b[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)(lds + L + sm_off(r0 + 16 * i + r16, 4 * s + g));
+    for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)sm_at(L, r0 >> 6, 16 * i + r16, 4 * s + g);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = *(const bf16x8*)(lds + R + sm_off(c0 + 16 * j + r16, 4 * s + g));
+    for (int j = 0; j < 2; ++j) b[j] = *(const bf16x8*)sm_at(R, c0 >> 6, (c0 & 63) + 16 * j + r16, 4 * s + g);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
   }
-  sm_finish(lds, acc, D, C, alpha, beta, r0, c0, lane);
+  sm_finish(acc, D, C, alpha, beta, r0, c0, lane);
 }
 
 // Q = Z + a·I on the first m rows (pan/optim/patch_muon.py:321-324: the
 // diagonal add in bf16); the padding rows and columns stay zero.
-__device__ __forceinline__ void sm_qinit(char* lds, int Z, int Q, float a, int m) {
+__device__ __forceinline__ void sm_qinit(const SmMat& Z, const SmMat& Q, float a, int m) {
 #pragma clang fp contract(off)
   for (int i = threadIdx.x; i < kSm * kSm / 8; i += blockDim.x) {
     const int r = i >> 4, c = i & 15;  // logical chunk c of row r: columns 8c .. 8c+7
-    u32x4 v = *(const u32x4*)(lds + Z + sm_off(r, c));
+    u32x4 v = *(const u32x4*)sm_at(Z, r >> 6, r & 63, c);
     const int e = r - 8 * c;  // the diagonal element's position in the chunk
     if (r < m && e >= 0 && e < 8) {
       const uint32_t w = v[e >> 1];
@@ -146,7 +176,7 @@ __device__ __forceinline__ void sm_qinit(char* lds, int Z, int Q, float a, int m
       const uint32_t qv = f2bf(bf2f(z) + a);
       v[e >> 1] = (e & 1) ? ((w & 0xffffu) | (qv << 16)) : ((w & 0xffff0000u) | qv);
     }
-    *(u32x4*)(lds + Q + sm_off(r, c)) = v;
+    *(u32x4*)sm_at(Q, r >> 6, r & 63, c) = v;
   }
   __syncthreads();
 }
@@ -164,144 +194,207 @@ __device__ __forceinline__ void wait_units(int n) {
   }
 }
 
-// One block of 8 waves per small matrix of the group (grid = matrices).
-__global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCoreArgs args) {
-#pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(1024))) char lds[4 * kSmMat];
-  constexpr int kR = 0, kZ = kSmMat, kQ = 2 * kSmMat, kRZ = 3 * kSmMat;
-  static_assert(kSmRing * kSmUnit == 4 * kSmMat, "the gram ring fills the LDS");
+// The gram ring: one __shared__ array per slot, so the compiler's LDS-DMA
+// tracking sees that reads of one slot do not wait for copies into the others.
+struct SmRing {
+  char* s[kSmRing];
+};
 
-  const MatDesc& d = args.descs[blockIdx.x];
-  const int wave = wave_id(), lane = lane_id();
-  const int r16 = lane & 15, g = lane >> 4;
-  const int r0 = (wave >> 2) * 64, c0 = (wave & 3) * 32;
-
-  // ---- R = X Xᵀ over k < Np in units of 64 k values: unit u is rows 0..127,
-  // bytes 128u .. 128u+127 of each row of X (ld Np); chunk c of row r of a unit
-  // is stored at chunk c ^ ((r >> 1) & 7), as in the grouped engine. A unit is
-  // 16 copies of 1 KiB (8 rows); wave w issues copies 2w and 2w+1.
-  const uint16_t* X = d.X[args.cur];
-  const int K = d.Np, KT = K / 64;
-  const __amdgpu_buffer_rsrc_t rsrc = panel_rsrc(X, (uint32_t)kSm * K * 2);
-  int voff[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {  // copy q = 2w + h: rows 8q + lane/8, stored chunk lane%8
-    const int q = 2 * wave + h;
-    const int sw = (4 * (q & 1) + (lane >> 4)) & 7;  // ((8q + lane/8) >> 1) & 7
-    voff[h] = (lane >> 3) * K * 2 + (((lane & 7) ^ sw) << 4);
-  }
-  auto copy_unit = [&](int u) {
-    char* dst = lds + (u % kSmRing) * kSmUnit;
+// Unit u of the gram, 64 k values: rows 0..127, bytes 128u .. 128u+127 of each
+// row of X (ld Np), 16 copies of 1 KiB (8 rows); wave w issues copies 2w and
+// 2w+1. Chunk c of row r is stored at chunk c ^ ((r >> 1) & 7), as in the
+// grouped engine.
+struct SmCopy {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int voff[2];  // lane offsets of copies 2w, 2w+1
+  int row8;     // bytes of 8 rows of X
+  int wave;
+  __device__ __forceinline__ void operator()(char* dst, int u) const {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int q = 2 * wave + h;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to_lds(dst + q * 1024), 16, voff[h], q * 8 * K * 2 + u * 128, 0,
-                                               0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to_lds(dst + q * 1024), 16, voff[h], q * row8 + u * 128, 0, 0);
     }
-  };
+  }
+};
+
+// One unit in slot S: wait for it, refill the slot read last (unit u-1's) with
+// unit u + 7, accumulate the unit's two k-steps. The barrier is a bare
+// s_barrier: __syncthreads' fence would drain every copy in flight.
+template <int S>
+__device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy, int u, int KT, f32x4 (&acc)[4][2],
+                                          int r0, int c0, int lane) {
+  wait_units(min(kSmRing - 2, KT - 1 - u));  // this wave's copies of unit u have landed
+  block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
+  if (u + kSmRing - 1 < KT) copy(ring.s[(S + kSmRing - 1) % kSmRing], u + kSmRing - 1);
+  const char* src = ring.s[S];
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int fo = r16 * 128 + (((4 * s + g) ^ ((r16 >> 1) & 7)) << 4);
+    bf16x8 a[4], b[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)(src + (r0 + 16 * i) * 128 + fo);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[j] = *(const bf16x8*)(src + (c0 + 16 * j) * 128 + fo);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
+  }
+}
+
+// One block of 8 waves per small matrix of the group (grid = matrices).
+__global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCoreArgs args) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) char g0[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g1[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g2[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g3[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g4[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g5[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g6[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char g7[kSmUnit];
+  SmRing ring;  // (set member by member: an aggregate initialiser of LDS addresses does not compile)
+  ring.s[0] = g0; ring.s[1] = g1; ring.s[2] = g2; ring.s[3] = g3;
+  ring.s[4] = g4; ring.s[5] = g5; ring.s[6] = g6; ring.s[7] = g7;
+  // after the gram the ring holds the M x M matrices, two slots each
+  SmMat R, Z, Q, RZ;
+  R.h[0] = g0; R.h[1] = g1; Z.h[0] = g2; Z.h[1] = g3;
+  Q.h[0] = g4; Q.h[1] = g5; RZ.h[0] = g6; RZ.h[1] = g7;
+
+  const MatDesc& d = args.descs[blockIdx.x];
+  const int wave = wave_id(), lane = lane_id();
+  const int r0 = (wave >> 2) * 64, c0 = (wave & 3) * 32;
+
+  // ---- R = X Xᵀ over k < Np
+  const int K = __builtin_amdgcn_readfirstlane(d.Np), KT = K / 64;
+  SmCopy copy;
+  copy.rsrc = uniform_rsrc(d.X[args.cur], (uint32_t)kSm * K * 2);
+  copy.row8 = 8 * K * 2;
+  copy.wave = wave;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // copy q = 2w + h: row 8q + lane/8, stored chunk lane%8
+    const int q = 2 * wave + h;
+    const int sw = (4 * (q & 1) + (lane >> 4)) & 7;  // ((8q + lane/8) >> 1) & 7
+    copy.voff[h] = (lane >> 3) * K * 2 + (((lane & 7) ^ sw) << 4);
+  }
   f32x4 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  for (int u = 0; u < kSmRing - 1 && u < KT; ++u) copy_unit(u);
-  for (int u = 0; u < KT; ++u) {
-    wait_units(min(kSmRing - 2, KT - 1 - u));  // this wave's copies of unit u have landed
-    __syncthreads();  // every wave's copies of u have landed; every wave is done with unit u-1
-    if (u + kSmRing - 1 < KT) copy_unit(u + kSmRing - 1);  // into unit u-1's slot
-    const char* src = lds + (u % kSmRing) * kSmUnit;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int fo = r16 * 128 + (((4 * s + g) ^ ((r16 >> 1) & 7)) << 4);
-      bf16x8 a[4], b[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)(src + (r0 + 16 * i) * 128 + fo);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = *(const bf16x8*)(src + (c0 + 16 * j) * 128 + fo);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
-    }
+  if (0 < KT) copy(ring.s[0], 0);
+  if (1 < KT) copy(ring.s[1], 1);
+  if (2 < KT) copy(ring.s[2], 2);
+  if (3 < KT) copy(ring.s[3], 3);
+  if (4 < KT) copy(ring.s[4], 4);
+  if (5 < KT) copy(ring.s[5], 5);
+  if (6 < KT) copy(ring.s[6], 6);
+  int u = 0;
+  for (; u + kSmRing <= KT; u += kSmRing) {
+    gram_unit<0>(ring, copy, u, KT, acc, r0, c0, lane);
+    gram_unit<1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
+    gram_unit<2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
+    gram_unit<3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
+    gram_unit<4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
+    gram_unit<5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
+    gram_unit<6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
+    gram_unit<7>(ring, copy, u + 7, KT, acc, r0, c0, lane);
   }
+  if (u < KT) gram_unit<0>(ring, copy, u, KT, acc, r0, c0, lane);
+  if (u + 1 < KT) gram_unit<1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
+  if (u + 2 < KT) gram_unit<2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
+  if (u + 3 < KT) gram_unit<3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
+  if (u + 4 < KT) gram_unit<4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
+  if (u + 5 < KT) gram_unit<5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
+  if (u + 6 < KT) gram_unit<6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
   // R = s²·X Xᵀ (s² = 1/‖X‖² on the unscaled first X): sm_finish's first
-  // barrier also ends every wave's reads of the ring, which R overwrites
-  sm_finish(lds, acc, kR, kR, args.first ? d.scales[0] : 1.0f, 0.0f, r0, c0, lane);
+  // barrier also ends every wave's reads of the ring, whose first two slots
+  // R overwrites (every copy has landed: the last unit waited for all)
+  sm_finish(acc, R, R, args.first ? d.scales[0] : 1.0f, 0.0f, r0, c0, lane);
 
   // ---- the M x M part of the iteration
-  int out = kZ;
+  const SmMat* out = &Z;
   if (args.steps == 0) {
     const float* k = args.coeffs + 3 * args.it0;
-    sm_product(lds, kR, kR, kR, kZ, k[2], k[1], wave, lane);  // B = c R R + b R
+    sm_product(R, R, R, Z, k[2], k[1], wave, lane);  // B = c R R + b R
   } else {
     for (int i = 0; i < args.steps; ++i) {
       const float* k = args.coeffs + 3 * (args.it0 + i);
       const float a = k[0], b = k[1], c = k[2];
-      sm_product(lds, kR, kR, kR, kZ, c, b, wave, lane);  // Z = c R R + b R
+      sm_product(R, R, R, Z, c, b, wave, lane);  // Z = c R R + b R
       if (i == 0)
-        sm_qinit(lds, kZ, kQ, a, d.M);  // Q = a I + Z
+        sm_qinit(Z, Q, a, d.M);  // Q = a I + Z
       else
-        sm_product(lds, kQ, kZ, kQ, kQ, 1.0f, a, wave, lane);  // Q = Q Z + a Q
+        sm_product(Q, Z, Q, Q, 1.0f, a, wave, lane);  // Q = Q Z + a Q
       if (i + 1 < args.steps) {
-        sm_product(lds, kR, kZ, kR, kRZ, 1.0f, a, wave, lane);   // RZ = R Z + a R
-        sm_product(lds, kZ, kRZ, kRZ, kR, 1.0f, a, wave, lane);  // R = Z RZ + a RZ
+        sm_product(R, Z, R, RZ, 1.0f, a, wave, lane);   // RZ = R Z + a R
+        sm_product(Z, RZ, RZ, R, 1.0f, a, wave, lane);  // R = Z RZ + a RZ
       }
     }
-    out = kQ;
+    out = &Q;
   }
 
   // ---- S (row-major 128 x 128) to the workspace
   uint16_t* S = d.S[args.so];
   for (int i = threadIdx.x; i < kSm * kSm / 8; i += blockDim.x) {
     const int r = i >> 4, c = i & 15;
-    *(u32x4*)(S + r * kSm + 8 * c) = *(const u32x4*)(lds + out + sm_off(r, c));
+    *(u32x4*)(S + r * kSm + 8 * c) = *(const u32x4*)sm_at(*out, r >> 6, r & 63, c);
   }
 }
 
-// X' = s·(a·X + S X) for one 128 x 256 tile of a small matrix per block
-// (prefix: Np / 256 tiles per matrix). A wide FINAL computes the transposed
-// tile X'ᵀ = Xᵀ Sᵀ (256 x 128; S is symmetric), whose quads are param rows, as
-// the grouped engine's FINAL does; every other tile is S X. K = 128 is loaded
-// whole into LDS; the epilogue is the grouped engine's, each wave standing in
-// for one wave of its 2 x 4 grid of 128 x 64 wave tiles.
+// Chunk c16 of row r of a flat LDS array of 256-byte rows, swizzled as in SmMat.
+__device__ __forceinline__ int sm_off(int r, int c16) { return r * kSmRow + ((c16 ^ (r & 15)) << 4); }
+
+// X' = s·(a·X + S X) for one tile of kSmApplyCols columns of a small matrix
+// per block (prefix: ceil(Np / kSmApplyCols) tiles per matrix). A wide FINAL
+// computes the transposed tile X'ᵀ = Xᵀ Sᵀ (kSmApplyCols x 128; S is
+// symmetric), whose quads are param rows, as the grouped engine's FINAL does;
+// every other tile is S X. K = 128 is loaded whole into LDS. Each wave owns
+// one 128 x 64 wave tile and finishes it with the grouped engine's epilogue,
+// standing in for the engine wave at the same place in a 256 x 256 tile.
 template <int STAGE, int PDT>
 __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(GemmArgs args) {
-  __shared__ __attribute__((aligned(1024))) char lds[3 * kSm * kSmRow];  // 96 KiB: 128 + 256 operand rows
+  __shared__ __attribute__((aligned(1024))) char lds[(kSm + kSmApplyCols) * kSmRow];
   const int t = blockIdx.x;
   const int m = find_matrix(args.prefix, args.n, t);
   const MatDesc& d = args.descs[m];
   const int lt = t - args.prefix[m];
   const int w = wave_id(), lane = lane_id();
   const bool wide_final = STAGE == ST_FINAL && !d.trans;
-  // rows of S (128) and rows 256·lt .. 256·lt+255 of Xᵀ (ld 128): 256 B each
+  // rows of S (128) and rows n0 .. n0 + kSmApplyCols - 1 of Xᵀ (ld 128), 256 B
+  // each; Xᵀ rows past Np read as zeros (buffer bounds)
+  const int n0 = lt * kSmApplyCols;
+  const int nx = min(kSmApplyCols, d.Np - n0);
   const uint16_t* S = d.S[args.sl];
-  const uint16_t* XT = d.XT[args.cur] + (int64_t)lt * kTile * kSm;
-  const uint16_t* Lsrc = wide_final ? XT : S;
-  const uint16_t* Rsrc = wide_final ? S : XT;
-  const int nL = wide_final ? kTile : kSm, nR = wide_final ? kSm : kTile;
-  char* lbuf = lds;
-  char* rbuf = lds + nL * kSmRow;
+  const uint16_t* XT = d.XT[args.cur] + (int64_t)n0 * kSm;
+  char* sbuf = lds;
+  char* xbuf = lds + kSm * kSmRow;
   {
     // copy q moves rows 4q .. 4q+3 (1 KiB): lane l lands at row 4q + l/16,
     // stored chunk l%16, so it loads logical chunk (l%16) ^ ((4q + l/16) & 15)
-    const __amdgpu_buffer_rsrc_t rl = panel_rsrc(Lsrc, (uint32_t)nL * kSmRow);
-    const __amdgpu_buffer_rsrc_t rr = panel_rsrc(Rsrc, (uint32_t)nR * kSmRow);
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(S, (uint32_t)kSm * kSmRow);
+    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(XT, (uint32_t)nx * kSmRow);
     const int row = lane >> 4;
-    for (int q = w; q < nL / 4; q += kSmApplyThreads / 64) {
+    for (int q = w; q < kSm / 4; q += kSmApplyWaves) {
       const int voff = row * kSmRow + (((lane & 15) ^ ((4 * q + row) & 15)) << 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, to_lds(lbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(sbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
     }
-    for (int q = w; q < nR / 4; q += kSmApplyThreads / 64) {
+    for (int q = w; q < kSmApplyCols / 4; q += kSmApplyWaves) {
       const int voff = row * kSmRow + (((lane & 15) ^ ((4 * q + row) & 15)) << 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, to_lds(rbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
     }
   }
   wait_vmcnt<0>();
   __syncthreads();
-  // waves in a 1 x 4 grid (S X, 128 x 256) or 2 x 2 (wide FINAL, 256 x 128);
-  // vw is the wave's index in the engine's 2 x 4 grid
-  const int vw = wide_final ? (w >> 1) * 4 + (w & 1) : w;
-  const int ar0 = (vw >> 2) * kWaveRows, bc0 = (vw & 3) * kWaveCols;
+  // S X: wave w owns columns n0 + 64w .. +63 (B = Xᵀ rows), all 128 rows (A = S).
+  // wide FINAL: wave w owns Xᵀ rows n0 + 128(w/2) .. +127 (A) and S rows
+  // 64(w%2) .. +63 (B).
+  const int xr = wide_final ? 128 * (w >> 1) : 64 * w;  // first Xᵀ row of the wave, tile-relative
+  if (xr >= nx) return;                                  // past Np: no barrier follows
+  const char* abuf = wide_final ? xbuf + xr * kSmRow : sbuf;
+  const char* bbuf = wide_final ? sbuf + 64 * (w & 1) * kSmRow : xbuf + xr * kSmRow;
   const int r16 = lane & 15, g = lane >> 4;
   f32x4 acc[kMi][kNi];
 #pragma unroll
@@ -312,17 +405,28 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
   for (int s = 0; s < 4; ++s) {
     bf16x8 b[kNi];
 #pragma unroll
-    for (int j = 0; j < kNi; ++j) b[j] = *(const bf16x8*)(rbuf + sm_off(bc0 + 16 * j + r16, 4 * s + g));
+    for (int j = 0; j < kNi; ++j) b[j] = *(const bf16x8*)(bbuf + sm_off(16 * j + r16, 4 * s + g));
 #pragma unroll
     for (int i = 0; i < kMi; ++i) {
-      const bf16x8 a = *(const bf16x8*)(lbuf + sm_off(ar0 + 16 * i + r16, 4 * s + g));
+      const bf16x8 a = *(const bf16x8*)(abuf + sm_off(16 * i + r16, 4 * s + g));
 #pragma unroll
       for (int j = 0; j < kNi; ++j) acc[i][j] = mfma_bf16(a, b[j], acc[i][j]);
     }
   }
+  // the engine wave at the same place: tile (ti, tj) of 256 x 256, wave index
+  // vw of its 2 x 4 grid of 128 x 64 wave tiles
+  const int xg = n0 + xr;  // first Xᵀ row (S X: first column) of this wave
   TileJob job{};
-  job.ti = wide_final ? lt : 0;
-  job.tj = wide_final ? 0 : lt;
+  int vw;
+  if (wide_final) {
+    job.ti = xg / kTile;
+    job.tj = 0;
+    vw = ((xg % kTile) / kWaveRows) * 4 + (w & 1);
+  } else {
+    job.ti = 0;
+    job.tj = xg / kTile;
+    vw = (xg % kTile) / kWaveCols;
+  }
   gemm_epilogue<STAGE, PDT>(args, d, job, acc, vw);
 }
 
