@@ -40,6 +40,19 @@ CONFIGS = {
 }
 CHUNKS = {6: 192}  # row blocks per param (adjust_lr_fn = (base, 0, n))
 
+# Not a BASELINE config: the AdamW half of PAN 2's step. The params Muon leaves
+# to AdamW (pan/optim/muon.py:12-92) in the 29B MMDiT (hidden 4096, 44 joint
+# blocks): per block the qkv / out / FFN biases, the q/k norm weights and the
+# text modulation vector (pan/models/transformers/pan_transformer.py:66-68,
+# :148, :205-212, :297), plus the embedders and the head (:732, :801; the
+# timestep MLP, patch embedding and output head shapes are approximations).
+H = 4096
+ADAMW_BLOCK = [(6 * H,), (2 * H,), (8 * H,), (H,), (4 * H,), (H,), (256,), (256,), (6 * H,)]
+ADAMW_GLOBAL = [(3, H), (H,), (H, H), (H,), (H, 256), (H,), (H, H), (H,), (H, 64), (H,), (64, H), (64,),
+                (2 * H, H), (2 * H,)]
+ADAMW_SET = ADAMW_BLOCK * 44 + ADAMW_GLOBAL
+CONFIGS[7] = ("adamw_pan2_set", [])
+
 
 def unit_shapes(config: int):
     """The matrices Newton–Schulz runs on: the params, or their row blocks."""
@@ -200,6 +213,118 @@ def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
     return 0
 
 
+def bench_adamw(args) -> int:
+    """One AdamW.step() over PAN 2's AdamW param set (fp32 params, grads and
+    state, tensor lr): libpanmuon's pm_adam_step behind torch's fused AdamW,
+    timed beside torch's own fused AdamW (the reference's GPU path) on the
+    same box."""
+    import math
+
+    import torch
+
+    import pan2_amd.optim.patch_adamw as pa
+    from pan2_amd import _lib
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    stock = pa._adam_module._fused_adam
+    steps = max(args.steps, 20)
+    warmup = max(args.warmup, 3)
+    gen = torch.Generator(device=device).manual_seed(7)
+    numel = sum(math.prod(s) for s in ADAMW_SET)
+    bytes_per_step = 28.0 * numel  # param r+w, grad r, exp_avg r+w, exp_avg_sq r+w (fp32)
+
+    def build():
+        ps = []
+        for shape in ADAMW_SET:
+            p = torch.nn.Parameter(torch.empty(shape, device=device))
+            p.data.normal_(0.0, 0.02, generator=gen)
+            p.grad = torch.empty(shape, device=device).normal_(0.0, 1e-3, generator=gen)
+            ps.append(p)
+        return torch.optim.AdamW(ps, lr=torch.tensor(1e-4, device=device), betas=(0.95, 0.95), eps=1e-8,
+                                 weight_decay=0.05, fused=True)
+
+    def timed(opt, fn):
+        pa._adam_module._fused_adam = fn
+        for _ in range(warmup):
+            opt.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            opt.step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    print(f"bench: AdamW set, {len(ADAMW_SET)} tensors, {numel} params", file=sys.stderr, flush=True)
+    try:
+        ref_ms = timed(build(), stock)
+        ours = build()
+        _lib.load()
+        pa._adam_module._fused_adam = pa._fused_adam
+        for _ in range(warmup):
+            ours.step()
+        torch.cuda.synchronize()
+        _lib.timing_enable(True)
+        _lib.timing_read()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ours.step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        recs = [r for r in _lib.timing_read() if r["kind"] == "adam"]
+        _lib.timing_enable(False)
+    finally:
+        pa._adam_module._fused_adam = stock
+    kern_ms = sum(r["ms"] for r in recs) / max(1, len(recs))
+    achieved = bytes_per_step / (kern_ms * 1e-3) / 1e9 if kern_ms > 0 else 0.0
+    cpu = None
+    if not args.no_cpu_baseline:
+        # torch's CPU AdamW (foreach) over the same set, one timed step after one warmup
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        cps = []
+        g = torch.Generator().manual_seed(7)
+        for shape in ADAMW_SET:
+            p = torch.nn.Parameter(torch.randn(shape, generator=g) * 0.02)
+            p.grad = torch.randn(shape, generator=g) * 1e-3
+            cps.append(p)
+        copt = torch.optim.AdamW(cps, lr=1e-4, betas=(0.95, 0.95), eps=1e-8, weight_decay=0.05, foreach=True)
+        copt.step()
+        t0 = time.perf_counter()
+        copt.step()
+        cms = (time.perf_counter() - t0) * 1e3
+        cpu = {"value": round(bytes_per_step / (cms * 1e-3) / 1e9, 2), "unit": "GB/s", "step_ms": round(cms, 2),
+               "cores": threads, "kind": "reference",
+               "sample": "torch.optim.AdamW(foreach=True) step on the host over the whole fp32 set (one step after "
+                         "a warmup step)"}
+    out = {
+        "metric": "AdamW step GB/s (algorithmic HBM bytes / step time), 1 GPU",
+        "value": round(bytes_per_step / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "adamw_pan2_set", "baseline_config": None, "tensors": len(ADAMW_SET),
+                   "params": numel, "param_dtype": "fp32", "grad_dtype": "fp32", "state_dtype": "fp32",
+                   "bytes_per_step": bytes_per_step},
+        "reference_gpu": {"what": "torch's own fused AdamW (torch._fused_adamw_) on the same box",
+                          "ms_per_step": round(ref_ms, 4),
+                          "value": round(bytes_per_step / (ref_ms * 1e-3) / 1e9, 2), "unit": "GB/s"},
+        "roofline": {"kernel": "pm_adam_kernel", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": None, "avg_launch_ms": round(kern_ms, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -232,6 +357,8 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU sharding is a design, not code", file=sys.stderr)
         return 2
+    if args.config == 7:
+        return bench_adamw(args)
 
     import torch
     import torch.optim._muon as torch_muon

@@ -214,6 +214,59 @@ int pm_gemm_symmetric(const void* left, const void* right, const void* addend, v
                       float alpha, float beta, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The Adam / AdamW half of PAN 2's step (pan/optim/muon.py:155-164 builds
+ * torch.optim.AdamW(fused=True) over the params Muon does not take). One
+ * contiguous tensor and its state; the fields mirror the lists torch's fused
+ * Adam receives (params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs,
+ * state_steps, torch/optim/adam.py:803-815).
+ *   step: torch's state["step"], a float32 scalar on the device.
+ *   max_exp_avg_sq: amsgrad only (NULL otherwise), dtype of exp_avg_sq.
+ */
+typedef struct pm_adam_tensor {
+  void* param;
+  void* grad; /* read; written (unscaled) only with a grad_scale */
+  void* exp_avg;
+  void* exp_avg_sq;
+  void* max_exp_avg_sq;
+  float* step;
+  int64_t numel;
+  int32_t param_dtype;
+  int32_t grad_dtype;
+  int32_t exp_avg_dtype;
+  int32_t exp_avg_sq_dtype;
+} pm_adam_tensor;
+
+/* The scalars of torch's Adam param group (torch/optim/adam.py:88-101). */
+typedef struct pm_adam_hparams {
+  double beta1;
+  double beta2;
+  double eps;
+  double weight_decay;
+  int32_t amsgrad;
+  int32_t maximize;
+  int32_t decoupled_weight_decay; /* 1: AdamW (param *= 1 - lr*wd), 0: Adam (grad += wd*param) */
+  int32_t reserved;
+} pm_adam_hparams;
+
+/*
+ * One Adam / AdamW step over n tensors, in place. Replaces torch's
+ * _fused_adam (torch/optim/adam.py:803-898): every step += 1, then per element
+ * (fp32 arithmetic, each result rounded once to its storage dtype)
+ *   p *= 1 - lr*wd (AdamW);  m = lerp(m, g, 1 - beta1);
+ *   v = v*beta2 + (1 - beta2) g^2;  p += -(lr / (1 - beta1^step)) * m / (sqrt(v) / sqrt(1 - beta2^step) + eps)
+ * (torch/optim/adam.py:414-547). lr from lr_dev (device float) when it is not
+ * NULL, else lr_host. grad_scale (device float, or NULL) divides the grads,
+ * which are written back unscaled, as torch's fused kernel leaves them;
+ * found_inf (device float, or NULL) skips the update and the step count when
+ * nonzero, as torch's fused path does for a GradScaler.
+ * Needs pm_adam_workspace_bytes(n) of device workspace (the descriptor table).
+ */
+size_t pm_adam_workspace_bytes(int n);
+int pm_adam_step(const pm_adam_tensor* tensors, int n, const pm_adam_hparams* hp, const float* lr_dev,
+                 double lr_host, const float* grad_scale, const float* found_inf, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/*
  * Opt-in launch timing (no counterpart in the reference, which has no
  * instrumentation; used by bench.py for live roofline figures). While enabled,
  * every launch of pm_muon_step / pm_newton_schulz records a HIP event on the
@@ -229,9 +282,10 @@ enum pm_kernel_kind {
   PM_K_UPDATE = 4,    /* X <- a X + B X (gram form: X <- Q X at the reset) */
   PM_K_FINAL = 5,     /* last update fused with the parameter step */
   PM_K_QINIT = 6,     /* gram form: Q = Z + a I */
-  PM_K_SMALL_CORE = 7 /* matrices with min(rows, cols) <= 128: gram and the
+  PM_K_SMALL_CORE = 7, /* matrices with min(rows, cols) <= 128: gram and the
                          M x M part of one iteration (standard form) or of one
                          segment (gram form), in one launch */
+  PM_K_ADAM = 8        /* pm_adam_step: step counts and the element update */
 };
 
 typedef struct pm_launch_time {

@@ -46,9 +46,11 @@ EXPORTS = (
     "pm_gemm_symmetric",
     "pm_timing_enable",
     "pm_timing_read",
+    "pm_adam_workspace_bytes",
+    "pm_adam_step",
 )
 
-KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit", "small_core")
+KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit", "small_core", "adam")
 
 
 class PmMatrix(ctypes.Structure):
@@ -107,6 +109,35 @@ class PmHparams(ctypes.Structure):
     ]
 
 
+class PmAdamTensor(ctypes.Structure):
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("exp_avg", ctypes.c_void_p),
+        ("exp_avg_sq", ctypes.c_void_p),
+        ("max_exp_avg_sq", ctypes.c_void_p),
+        ("step", ctypes.c_void_p),
+        ("numel", ctypes.c_int64),
+        ("param_dtype", ctypes.c_int32),
+        ("grad_dtype", ctypes.c_int32),
+        ("exp_avg_dtype", ctypes.c_int32),
+        ("exp_avg_sq_dtype", ctypes.c_int32),
+    ]
+
+
+class PmAdamHparams(ctypes.Structure):
+    _fields_ = [
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("eps", ctypes.c_double),
+        ("weight_decay", ctypes.c_double),
+        ("amsgrad", ctypes.c_int32),
+        ("maximize", ctypes.c_int32),
+        ("decoupled_weight_decay", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 class PmLaunchTime(ctypes.Structure):
     _fields_ = [
         ("kind", ctypes.c_int32),
@@ -154,6 +185,9 @@ def load() -> ctypes.CDLL:
             "pm_gemm_symmetric": (ctypes.c_int, [vp, vp, vp, vp, i64, f32, f32, vp, sz, vp]),
             "pm_timing_enable": (ctypes.c_int, [ctypes.c_int]),
             "pm_timing_read": (ctypes.c_int, [ctypes.POINTER(PmLaunchTime), ctypes.c_int]),
+            "pm_adam_workspace_bytes": (sz, [ctypes.c_int]),
+            "pm_adam_step": (ctypes.c_int, [ctypes.POINTER(PmAdamTensor), ctypes.c_int, ctypes.POINTER(PmAdamHparams),
+                                            vp, f64, vp, vp, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -424,6 +458,111 @@ def gemm_symmetric(left: torch.Tensor, right: torch.Tensor, addend: torch.Tensor
                                    float(alpha), float(beta), ws.data_ptr(), nbytes, stream_of(left.device))
     check(rc, "pm_gemm_symmetric")
     return out
+
+
+def _device_scalar(t, what: str, dev):
+    """Pointer of a 1-element float32 device tensor (or None)."""
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor) or t.numel() != 1 or t.dtype != torch.float32 or t.device != dev:
+        raise ValueError(f"{what} must be a 1-element float32 tensor on {dev}")
+    return t.data_ptr()
+
+
+# numpy twin of PmAdamTensor, filled list by list
+_PM_ADAM_NP = np.dtype({
+    "names": [f for f, _ in PmAdamTensor._fields_],
+    "formats": ["u8", "u8", "u8", "u8", "u8", "u8", "i8", "i4", "i4", "i4", "i4"],
+    "offsets": [getattr(PmAdamTensor, f).offset for f, _ in PmAdamTensor._fields_],
+    "itemsize": ctypes.sizeof(PmAdamTensor),
+})
+
+
+def _dtype_codes(ts) -> int | list[int]:
+    kinds = {t.dtype for t in ts}
+    if len(kinds) == 1:
+        t = ts[0]
+        return dtype_code(t)
+    return [dtype_code(t) for t in ts]
+
+
+def _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev):
+    for i, p in enumerate(params):
+        x = max_exp_avg_sqs[i] if amsgrad else None
+        named = ((grads[i], "grad"), (exp_avgs[i], "exp_avg"), (exp_avg_sqs[i], "exp_avg_sq"))
+        for t, what in ((p, "param"),) + named + (((x, "max_exp_avg_sq"),) if amsgrad else ()):
+            if t.device != dev:
+                raise ValueError("all tensors of one call must be on one device")
+            if not t.is_contiguous():
+                raise ValueError(f"{what} must be contiguous")
+            if t.shape != p.shape:
+                raise ValueError(f"{what} shape {tuple(t.shape)} differs from the param's {tuple(p.shape)}")
+        st = state_steps[i]
+        if st.device != dev or st.dtype != torch.float32 or st.numel() != 1:
+            raise ValueError("state steps must be 1-element float32 tensors on the params' device")
+        if amsgrad and x.dtype != exp_avg_sqs[i].dtype:
+            raise ValueError("max_exp_avg_sq must have exp_avg_sq's dtype")
+
+
+def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, *, lr, beta1: float,
+              beta2: float, eps: float, weight_decay: float, amsgrad: bool, maximize: bool, decoupled: bool,
+              grad_scale=None, found_inf=None, trusted: bool = False) -> None:
+    """pm_adam_step over matching lists of contiguous device tensors (updated
+    in place, steps included). lr: float, or a 1-element tensor (read on the
+    device when it lives there). trusted: the lists come from torch's Adam,
+    whose _init_group already guarantees one device, matching shapes,
+    contiguous state and float32 device steps; only the per-call checks run."""
+    lib = load()
+    n = len(params)
+    if n == 0:
+        return
+    dev = params[0].device
+    if not params[0].is_cuda:
+        raise RuntimeError("pan2_amd Adam runs on HIP device tensors only; got a CPU parameter")
+    if not trusted:
+        _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev)
+    elif any(not g.is_contiguous() for g in grads):
+        raise ValueError("grads must be contiguous")
+    arr = np.zeros(n, dtype=_PM_ADAM_NP)
+    arr["param"] = [t.data_ptr() for t in params]
+    arr["grad"] = [t.data_ptr() for t in grads]
+    arr["exp_avg"] = [t.data_ptr() for t in exp_avgs]
+    arr["exp_avg_sq"] = [t.data_ptr() for t in exp_avg_sqs]
+    if amsgrad:
+        arr["max_exp_avg_sq"] = [t.data_ptr() for t in max_exp_avg_sqs]
+    arr["step"] = [t.data_ptr() for t in state_steps]
+    arr["numel"] = [t.numel() for t in params]
+    arr["param_dtype"] = _dtype_codes(params)
+    arr["grad_dtype"] = _dtype_codes(grads)
+    arr["exp_avg_dtype"] = _dtype_codes(exp_avgs)
+    arr["exp_avg_sq_dtype"] = _dtype_codes(exp_avg_sqs)
+    keep = [arr]
+    hp = PmAdamHparams(beta1=float(beta1), beta2=float(beta2), eps=float(eps), weight_decay=float(weight_decay),
+                       amsgrad=int(bool(amsgrad)), maximize=int(bool(maximize)),
+                       decoupled_weight_decay=int(bool(decoupled)))
+    lr_dev, lr_host = None, 0.0
+    if isinstance(lr, torch.Tensor):
+        if lr.numel() != 1:
+            raise ValueError("Tensor lr must be 1-element")
+        if lr.device.type == "cpu":
+            lr_host = float(lr.item())
+        else:
+            if lr.device != dev:
+                raise ValueError("lr tensor must be on the params' device")
+            lr_t = lr.reshape(()).to(torch.float32)
+            keep.append(lr_t)
+            lr_dev = lr_t.data_ptr()
+    else:
+        lr_host = float(lr)
+    gs = _device_scalar(grad_scale, "grad_scale", dev)
+    fi = _device_scalar(found_inf, "found_inf", dev)
+    with torch.cuda.device(dev):
+        nbytes = lib.pm_adam_workspace_bytes(n)
+        ws = workspace(nbytes, dev)
+        rc = lib.pm_adam_step(arr.ctypes.data_as(ctypes.POINTER(PmAdamTensor)), n, ctypes.byref(hp), lr_dev,
+                              lr_host, gs, fi, ws.data_ptr(), nbytes, stream_of(dev))
+    check(rc, "pm_adam_step")
+    del keep
 
 
 def timing_enable(on: bool = True) -> None:

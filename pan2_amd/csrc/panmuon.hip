@@ -16,6 +16,7 @@
 #include "../../include/panmuon.h"
 #include "pm_kernels.hpp"
 #include "pm_small.hpp"
+#include "pm_adam.hpp"
 
 using namespace pm;
 
@@ -24,6 +25,8 @@ static_assert(sizeof(MatDesc) % 8 == 0, "descriptor alignment");
 static_assert(sizeof(pm_matrix) == 88, "pm_matrix layout");
 static_assert(sizeof(pm_ns_matrix) == 56, "pm_ns_matrix layout");
 static_assert(sizeof(pm_hparams) == 56, "pm_hparams layout");
+static_assert(sizeof(pm_adam_tensor) == 72, "pm_adam_tensor layout");
+static_assert(sizeof(pm_adam_hparams) == 48, "pm_adam_hparams layout");
 
 namespace {
 
@@ -887,6 +890,91 @@ int pm_gemm_symmetric(const void* left, const void* right, const void* addend, v
   hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_SYMM>, dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PM_OK : hip_fail(e, "symmetric product launch");
+}
+
+// Descriptor table of an Adam call: descs[n] | chunk prefix[n+1].
+size_t pm_adam_workspace_bytes(int n) {
+  if (n < 0) return 0;
+  return align_up((size_t)n * sizeof(AdamDesc)) + align_up((size_t)(n + 1) * 4);
+}
+
+int pm_adam_step(const pm_adam_tensor* ts, int n, const pm_adam_hparams* hp, const float* lr_dev, double lr_host,
+                 const float* grad_scale, const float* found_inf, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_err.clear();
+  if (n < 0 || (n > 0 && !ts)) return fail(PM_EINVAL, "bad tensor list");
+  if (!hp) return fail(PM_EINVAL, "hparams is NULL");
+  if (n == 0) return PM_OK;
+  if (!(hp->beta1 >= 0.0 && hp->beta1 < 1.0) || !(hp->beta2 >= 0.0 && hp->beta2 < 1.0))
+    return fail(PM_EINVAL, "betas must be in [0, 1)");
+  if (!(hp->eps >= 0.0)) return fail(PM_EINVAL, "eps must be >= 0");
+  if (!(hp->weight_decay >= 0.0)) return fail(PM_EINVAL, "weight_decay must be >= 0");
+  const size_t need = pm_adam_workspace_bytes(n);
+  if (!workspace) return fail(PM_EINVAL, "workspace is NULL");
+  if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
+  if (workspace_bytes < need) return fail(PM_EWORKSPACE, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  std::vector<char> host(need, 0);
+  AdamDesc* descs = (AdamDesc*)host.data();
+  int32_t* prefix = (int32_t*)(host.data() + align_up((size_t)n * sizeof(AdamDesc)));
+  prefix[0] = 0;
+  for (int i = 0; i < n; ++i) {
+    const pm_adam_tensor& t = ts[i];
+    if (t.numel < 0) return fail(PM_EINVAL, "tensor %d: negative numel", i);
+    if (!t.step) return fail(PM_EINVAL, "tensor %d: NULL step", i);
+    if (t.numel > 0 && (!t.param || !t.grad || !t.exp_avg || !t.exp_avg_sq))
+      return fail(PM_EINVAL, "tensor %d: NULL tensor pointer", i);
+    if (hp->amsgrad && t.numel > 0 && !t.max_exp_avg_sq) return fail(PM_EINVAL, "tensor %d: amsgrad needs max_exp_avg_sq", i);
+    if (!valid_dtype(t.param_dtype) || !valid_dtype(t.grad_dtype) || !valid_dtype(t.exp_avg_dtype) ||
+        !valid_dtype(t.exp_avg_sq_dtype))
+      return fail(PM_EDTYPE, "tensor %d: dtypes must be f32 or bf16", i);
+    const int64_t chunks = (t.numel + kAdamChunk - 1) / kAdamChunk;
+    if (prefix[i] + chunks > INT32_MAX) return fail(PM_EINVAL, "too many elements in one call");
+    prefix[i + 1] = (int32_t)(prefix[i] + chunks);
+    AdamDesc& d = descs[i];
+    d.p = t.param; d.g = (void*)t.grad; d.m = t.exp_avg; d.v = t.exp_avg_sq;
+    d.vmax = hp->amsgrad ? t.max_exp_avg_sq : nullptr;
+    d.step = t.step;
+    d.n = t.numel;
+    d.p_dt = t.param_dtype; d.g_dt = t.grad_dtype; d.m_dt = t.exp_avg_dtype; d.v_dt = t.exp_avg_sq_dtype;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  int rc = upload(host.data(), need, workspace, s);
+  if (rc) return rc;
+  const AdamDesc* ddesc = (const AdamDesc*)workspace;
+  AdamArgs a{};
+  a.descs = ddesc;
+  a.prefix = (const int32_t*)((char*)workspace + ((char*)prefix - host.data()));
+  a.n = n;
+  a.b1d = hp->beta1;
+  a.b2d = hp->beta2;
+  a.beta2 = (float)hp->beta2;
+  a.w1 = (float)(1.0 - hp->beta1);
+  a.w2 = (float)(1.0 - hp->beta2);
+  a.eps = (float)hp->eps;
+  a.wd = (float)hp->weight_decay;
+  a.wdd = hp->weight_decay;
+  a.amsgrad = hp->amsgrad != 0;
+  a.maximize = hp->maximize != 0;
+  a.decoupled = hp->decoupled_weight_decay != 0;
+  a.lr_dev = lr_dev;
+  a.lr_host = lr_host;
+  a.grad_scale = grad_scale;
+  a.found_inf = found_inf;
+  timing_begin(s);
+  hipLaunchKernelGGL(pm_adam_count_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, s, ddesc, n,
+                     found_inf);
+  if (prefix[n] > 0) hipLaunchKernelGGL(pm_adam_kernel, dim3(prefix[n]), dim3(kThreads), 0, s, a);
+  double bytes = 0;
+  for (int i = 0; i < n; ++i) {
+    const pm_adam_tensor& t = ts[i];
+    auto sz = [](int32_t dt) { return dt == PM_DTYPE_F32 ? 4.0 : 2.0; };
+    const double per = 2 * sz(t.param_dtype) + sz(t.grad_dtype) + 2 * sz(t.exp_avg_dtype) +
+                       (hp->amsgrad ? 4 : 2) * sz(t.exp_avg_sq_dtype);
+    bytes += per * (double)t.numel;
+  }
+  timing_mark(s, PM_K_ADAM, 0, -1, n, 0.0, bytes);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "adam launch");
 }
 
 }  // extern "C"

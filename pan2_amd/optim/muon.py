@@ -2,7 +2,8 @@
 
 Same names, arguments, return value and errors as the reference factory
 (pan/optim/muon.py:12-178). The only difference is what a tensor lr installs:
-:func:`pan2_amd.optim.patch_muon.patch_muon`, whose step runs on libpanmuon.
+:func:`pan2_amd.optim.patch_muon.patch_muon` and
+:func:`pan2_amd.optim.patch_adamw.patch_adamw`, whose steps run on libpanmuon.
 """
 from __future__ import annotations
 
@@ -11,6 +12,7 @@ from typing import Dict, List, Tuple
 
 import torch
 
+from .patch_adamw import patch_adamw
 from .patch_lr_scheduler import patch_lr_scheduler
 from .patch_muon import patch_muon
 
@@ -83,9 +85,9 @@ def build_native_muon_optimizers(
 
     Returns {"optimizers": {"muon": ..., "adamw": ...} (absent keys omitted),
     "stats": split summary, "param_names": {"muon", "adamw", "muon_chunked"}}.
-    A tensor ``lr`` installs the libpanmuon step (and the host-side
-    get_last_lr); a float lr leaves torch's stock Muon in place, as the
-    reference does (:126-128). ``muon_chunks`` maps a param name to
+    A tensor ``lr`` installs the libpanmuon steps (Muon, and the fused AdamW
+    behind the AdamW half) and the host-side get_last_lr; a float lr leaves
+    torch's stock Muon in place, as the reference does (:126-128). ``muon_chunks`` maps a param name to
     (chunk_dim, n_chunks); each distinct pair becomes its own param group whose
     ``adjust_lr_fn`` is (muon_adjust_lr_fn, dim, n_chunks) (:130-146).
     """
@@ -118,6 +120,8 @@ def build_native_muon_optimizers(
             groups, lr=_lr(), weight_decay=weight_decay, momentum=momentum, adjust_lr_fn=muon_adjust_lr_fn,
         )
     if adamw_named:
+        if tensor_lr:
+            patch_adamw()
         optimizers["adamw"] = torch.optim.AdamW(
             adamw_named, lr=_lr(), betas=adamw_betas, eps=adamw_eps, weight_decay=weight_decay,
             capturable=capturable, fused=True,

@@ -1,0 +1,91 @@
+"""The AdamW half of PAN 2's optimizer step on MI355X, installed over torch's
+fused Adam by :func:`patch_adamw`.
+
+PAN 2 builds ``torch.optim.AdamW(fused=True)`` over the params Muon does not
+take (pan/optim/muon.py:155-164). ``AdamW.step`` reaches the module-global
+``_fused_adam`` of the torch.optim.adam module (TORCH/optim/adam.py:963-964,
+:803-898);
+:func:`patch_adamw` replaces it with a keyword-compatible function that hands
+every tensor of the group to libpanmuon's ``pm_adam_step`` in one call: the
+step counts and the element update run as two HIP launches on the current
+stream, with no host synchronisation. The optimizer object, its param groups
+and its state (``step``, ``exp_avg``, ``exp_avg_sq``) stay torch's, so
+state_dict and checkpoints are unchanged.
+"""
+from __future__ import annotations
+
+import importlib
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+
+# torch.optim does not keep its adam submodule as an attribute
+_adam_module = importlib.import_module("torch.optim.adam")
+
+
+def _scalar(x):
+    """A 1-element tensor beta becomes a Python float (torch's _to_scalar)."""
+    return x.item() if isinstance(x, Tensor) else x
+
+
+@torch.compiler.disable
+def _fused_adam(
+    params: list[Tensor],
+    grads: list[Tensor],
+    exp_avgs: list[Tensor],
+    exp_avg_sqs: list[Tensor],
+    max_exp_avg_sqs: list[Tensor],
+    state_steps: list[Tensor],
+    grad_scale: Tensor | None,
+    found_inf: Tensor | None,
+    *,
+    amsgrad: bool,
+    has_complex: bool,
+    beta1,
+    beta2,
+    lr,
+    weight_decay: float,
+    eps: float,
+    maximize: bool,
+    capturable: bool,
+    differentiable: bool,
+    decoupled_weight_decay: bool,
+) -> None:
+    """Keyword-compatible replacement of TORCH/optim/adam.py:803-898 (one call per device)."""
+    if not params:
+        return
+    if differentiable:
+        raise RuntimeError("Adam with fused=True does not support differentiable=True")
+    if has_complex:
+        raise NotImplementedError("pan2_amd Adam has no complex-parameter path")
+    beta1, beta2 = _scalar(beta1), _scalar(beta2)
+    by_device: dict[torch.device, list[int]] = {}
+    for i, p in enumerate(params):
+        if not p.is_cuda:
+            raise RuntimeError("pan2_amd Adam runs on HIP device tensors only; got a CPU parameter")
+        by_device.setdefault(p.device, []).append(i)
+    for dev, idx in by_device.items():
+        pick = lambda xs: [xs[i] for i in idx]  # noqa: E731
+        dev_lr = lr
+        if isinstance(lr, Tensor) and lr.device.type != "cpu" and lr.device != dev:
+            dev_lr = lr.to(device=dev, non_blocking=True)
+        _lib.adam_step(
+            pick(params), pick(grads), pick(exp_avgs), pick(exp_avg_sqs),
+            pick(max_exp_avg_sqs) if amsgrad else [None] * len(idx), pick(state_steps),
+            lr=dev_lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+            maximize=maximize, decoupled=decoupled_weight_decay,
+            grad_scale=None if grad_scale is None else grad_scale.to(dev, non_blocking=True),
+            found_inf=None if found_inf is None else found_inf.to(dev, non_blocking=True),
+            trusted=True,
+        )
+
+
+def patch_adamw() -> None:
+    """Install the HIP path behind every ``fused=True`` Adam / AdamW step.
+
+    Loads libpanmuon first, so a missing or broken build fails here, loudly.
+    """
+    _lib.load()
+    _adam_module._fused_adam = _fused_adam

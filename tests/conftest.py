@@ -58,3 +58,25 @@ def torch_stock_muon():
             _torch_muon._zeropower_via_newtonschulz, _torch_muon._single_tensor_muon = saved
 
     return stock
+
+# torch's own fused Adam, captured before patch_adamw replaces the module global
+import torch.optim.adam as _torch_adam  # noqa: E402
+
+TORCH_FUSED_ADAM = _torch_adam._fused_adam
+
+
+@pytest.fixture
+def torch_fused_adam():
+    """Run a block with torch's own fused Adam installed, restoring after."""
+    import contextlib
+
+    @contextlib.contextmanager
+    def stock():
+        saved = _torch_adam._fused_adam
+        _torch_adam._fused_adam = TORCH_FUSED_ADAM
+        try:
+            yield
+        finally:
+            _torch_adam._fused_adam = saved
+
+    return stock

@@ -270,3 +270,83 @@ def check_muon_step_vs_torch(ref):
         o_t = (p0.numpy().astype(np.float64) * (1 - 0.02 * 0.01) - p.detach().numpy()) / adj
         assert rel(ref_o, o_t) < 1.5e-2, (adjust, rel(ref_o, o_t))
         assert np.abs(ref_p - p.detach().numpy()).max() <= 2e-2 * adj, (adjust,)
+
+
+# ------------------------------------------------------------------ Adam / AdamW
+
+ADAM_CASES = [
+    # (decoupled, weight_decay, amsgrad, maximize, betas)
+    (True, 0.05, False, False, (0.95, 0.95)),   # PAN 2's AdamW (pan/optim/muon.py:155-164, train.py:240)
+    (True, 0.0, False, False, (0.9, 0.999)),
+    (False, 0.01, False, False, (0.9, 0.999)),  # Adam: L2 decay folded into the grad
+    (True, 0.1, True, False, (0.8, 0.99)),
+    (True, 0.01, False, True, (0.3, 0.6)),     # maximize; 1 - beta1 >= 0.5 takes lerp's other branch
+]
+
+
+def _adam_torch_cpu(p0, grads, *, lr, betas, eps, wd, decoupled, amsgrad, maximize):
+    """torch's single-tensor Adam / AdamW on the CPU (TORCH/optim/adam.py:347-549)."""
+    p = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+    cls = torch.optim.AdamW if decoupled else torch.optim.Adam
+    opt = cls([p], lr=lr, betas=betas, eps=eps, weight_decay=wd, amsgrad=amsgrad, maximize=maximize,
+              foreach=False, fused=False)
+    for g in grads:
+        p.grad = torch.from_numpy(g.copy())
+        opt.step()
+    st = opt.state[p]
+    vmax = st["max_exp_avg_sq"].numpy() if amsgrad else None
+    return p.detach().numpy(), st["exp_avg"].numpy(), st["exp_avg_sq"].numpy(), vmax, float(st["step"])
+
+
+def check_adam_vs_torch(ref):
+    """Three steps of the oracle against torch's CPU Adam / AdamW: the same
+    arithmetic up to torch's vectorised lerp fusing its multiply-add (a few
+    fp32 ulps)."""
+    rng = np.random.default_rng(5)
+    lr, eps = 3e-3, 1e-8
+    for decoupled, wd, amsgrad, maximize, betas in ADAM_CASES:
+        p0 = rng.standard_normal(997).astype(np.float32)
+        grads = [(rng.standard_normal(997) * 10.0 ** rng.uniform(-3, 1)).astype(np.float32) for _ in range(3)]
+        tp, tm, tv, tx, tstep = _adam_torch_cpu(p0, grads, lr=lr, betas=betas, eps=eps, wd=wd, decoupled=decoupled,
+                                                amsgrad=amsgrad, maximize=maximize)
+        p, m, v = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+        x = np.zeros_like(p0) if amsgrad else None
+        step = 0.0
+        for g in grads:
+            p, m, v, x, step = ref.adam_step(p, g, m, v, step, lr=lr, beta1=betas[0], beta2=betas[1], eps=eps,
+                                             weight_decay=wd, decoupled=decoupled, amsgrad=amsgrad,
+                                             max_exp_avg_sq=x, maximize=maximize)
+        case = (decoupled, wd, amsgrad, maximize, betas)
+        assert step == tstep, case
+
+        def close(a, b, what):
+            # a few ulps of the array's scale: a moment near zero comes from cancelling terms
+            assert np.all(np.abs(a - b) <= 2e-6 * np.abs(b) + 1e-6 * np.abs(b).max()), (what, case)
+
+        close(m, tm, "exp_avg")
+        close(v, tv, "exp_avg_sq")
+        if amsgrad:
+            close(x, tx, "max_exp_avg_sq")
+        # the update is lr-sized: its fp32 error is a few ulps of lr, plus p's own rounding
+        assert np.all(np.abs(p - tp) <= 2e-6 * np.abs(tp) + 2e-6 * lr), case
+
+
+def check_adam_closed_form(ref):
+    """First AdamW step from zero state: the bias corrections cancel the
+    moment weights, so p1 = p0 (1 - lr wd) - lr g / (|g| + eps)."""
+    rng = np.random.default_rng(9)
+    p0 = rng.standard_normal(513).astype(np.float32)
+    g = (rng.standard_normal(513) * 1e-2).astype(np.float32)
+    lr, wd, eps = 1e-3, 0.05, 1e-8
+    p, m, v, _, step = ref.adam_step(p0, g, np.zeros_like(p0), np.zeros_like(p0), 0.0, lr=lr, beta1=0.95, beta2=0.95,
+                                     eps=eps, weight_decay=wd)
+    assert step == 1.0
+    g64 = g.astype(np.float64)
+    want = p0.astype(np.float64) * (1 - lr * wd) - lr * g64 / (np.abs(g64) + eps)
+    assert np.all(np.abs(p - want) <= 4e-7 * np.abs(want) + 1e-6 * lr), float(np.abs(p - want).max())
+    np.testing.assert_allclose(m, 0.05 * g64, rtol=1e-6)
+    np.testing.assert_allclose(v, 0.05 * g64 * g64, rtol=1e-6)
+    # zero grad and no decay: nothing moves
+    p2, *_ = ref.adam_step(p0, np.zeros_like(p0), np.zeros_like(p0), np.zeros_like(p0), 0.0, lr=lr, beta1=0.9,
+                           beta2=0.999, eps=eps, weight_decay=0.0)
+    assert np.array_equal(p2, p0)

@@ -65,6 +65,8 @@ STRUCTS = {
     "pm_ns_matrix": _lib.PmNsMatrix,
     "pm_hparams": _lib.PmHparams,
     "pm_launch_time": _lib.PmLaunchTime,
+    "pm_adam_tensor": _lib.PmAdamTensor,
+    "pm_adam_hparams": _lib.PmAdamHparams,
 }
 # ctypes field name -> C field name where Python needs another spelling
 RENAME = {"in_": "in"}
@@ -185,6 +187,45 @@ def test_gemm_symmetric_argument_errors(lib):
     assert lib.pm_gemm_symmetric(None, FAKE, FAKE, FAKE, 256, 1.0, 0.5, FAKE, ws, None) == _lib.PM_EINVAL
     assert lib.pm_gemm_symmetric(FAKE, FAKE, FAKE, FAKE, 256, 1.0, 0.5, FAKE, ws - 1, None) == _lib.PM_EWORKSPACE
     assert lib.pm_gemm_symmetric(FAKE, FAKE, FAKE, FAKE, 256, 1.0, 0.5, FAKE + 8, ws, None) == _lib.PM_EINVAL
+
+
+def adam_tensor(numel=1000, dts=(0, 0, 0, 0), ptrs=(FAKE,) * 4, step=FAKE, vmax=None):
+    t = _lib.PmAdamTensor()
+    t.param, t.grad, t.exp_avg, t.exp_avg_sq = ptrs
+    t.max_exp_avg_sq = vmax
+    t.step = step
+    t.numel = numel
+    t.param_dtype, t.grad_dtype, t.exp_avg_dtype, t.exp_avg_sq_dtype = dts
+    return t
+
+
+def test_adam_argument_errors(lib):
+    def run(ts, ws=FAKE, ws_bytes=1 << 30, **kw):
+        hp = _lib.PmAdamHparams(beta1=kw.get("beta1", 0.9), beta2=kw.get("beta2", 0.999), eps=1e-8,
+                                weight_decay=kw.get("wd", 0.01), amsgrad=kw.get("amsgrad", 0), maximize=0,
+                                decoupled_weight_decay=1)
+        a = (_lib.PmAdamTensor * len(ts))(*ts) if ts else None
+        return lib.pm_adam_step(a, len(ts), ctypes.byref(hp), None, 1e-3, None, None, ws, ws_bytes, None)
+
+    assert lib.pm_adam_workspace_bytes(-1) == 0
+    assert lib.pm_adam_workspace_bytes(3) > 0
+    assert run([]) == 0
+    assert run([adam_tensor()], beta1=1.0) == _lib.PM_EINVAL
+    assert "betas" in _lib.last_error()
+    assert run([adam_tensor()], wd=-1.0) == _lib.PM_EINVAL
+    assert run([adam_tensor(numel=-1)]) == _lib.PM_EINVAL
+    assert run([adam_tensor(step=None)]) == _lib.PM_EINVAL
+    assert run([adam_tensor(ptrs=(FAKE, 0, FAKE, FAKE))]) == _lib.PM_EINVAL
+    assert run([adam_tensor()], amsgrad=1) == _lib.PM_EINVAL
+    assert "max_exp_avg_sq" in _lib.last_error()
+    assert run([adam_tensor(dts=(0, 2, 0, 0))]) == _lib.PM_EDTYPE
+    assert run([adam_tensor()], ws=0) == _lib.PM_EINVAL
+    assert run([adam_tensor()], ws=FAKE + 8) == _lib.PM_EINVAL
+    assert run([adam_tensor()], ws_bytes=16) == _lib.PM_EWORKSPACE
+    hp = _lib.PmAdamHparams()
+    assert lib.pm_adam_step(None, 2, ctypes.byref(hp), None, 1e-3, None, None, FAKE, 1 << 30, None) == _lib.PM_EINVAL
+    assert lib.pm_adam_step((_lib.PmAdamTensor * 1)(adam_tensor()), 1, None, None, 1e-3, None, None, FAKE, 1 << 30,
+                            None) == _lib.PM_EINVAL
 
 
 def test_error_text_is_per_thread(lib):

@@ -127,3 +127,15 @@ def test_golden_matches_current_torch(golden):
         got = TORCH_ZEROPOWER(G.clone(), pins.COEFFS, 5, 1e-7).float().numpy()
         want = bf16.from_bf16_bits(golden[f"ns/{c}/out_bf16"])
         assert pins.rel(got, want) < 1e-2, c
+
+
+def test_adam_vs_torch_cpu():
+    from oracle import adamw_ref
+
+    pins.check_adam_vs_torch(adamw_ref)
+
+
+def test_adam_closed_form():
+    from oracle import adamw_ref
+
+    pins.check_adam_closed_form(adamw_ref)

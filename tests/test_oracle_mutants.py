@@ -89,3 +89,33 @@ def test_unmutated_copy_passes_every_check():
     for check in MUON_CHECKS:
         check(mod)
     pins.check_round_bf16(_mutant(oracle.bf16, "import numpy as np", "import numpy as np", "identity_bf16"))
+
+
+ADAM_CHECKS = (pins.check_adam_vs_torch, pins.check_adam_closed_form)
+
+ADAM_MUTANTS = [
+    ("betas_swapped", "m = lerp(m, gr, 1 - beta1)", "m = lerp(m, gr, 1 - beta2)"),
+    ("no_first_bias_correction", "step_size = lr / bc1", "step_size = lr"),
+    ("second_correction_not_rooted", "bc2_sqrt = bc2 ** 0.5", "bc2_sqrt = bc2"),
+    ("step_not_incremented", "step = float(f32(step) + f32(1))", "step = float(f32(step) + f32(2))"),
+    ("adamw_decay_coupled", "p = p * f32(1 - lr * weight_decay)", "gr = gr + f32(weight_decay) * p"),
+    ("eps_inside_sqrt", "np.sqrt(vh) / f32(bc2_sqrt) + f32(eps)", "np.sqrt(vh + f32(eps)) / f32(bc2_sqrt)"),
+    ("update_sign", "p = p + f32(-step_size)", "p = p + f32(step_size)"),
+    ("lerp_upper_branch", "return end - (end - start) * (f32(1) - w)", "return end - (end - start) * w"),
+    ("maximize_ignored", "gr = -g if maximize else g", "gr = g"),
+    ("amsgrad_uses_current_v", "        vh = vmax\n", "        vh = v\n"),
+]
+
+
+@pytest.mark.parametrize("name,old,new", ADAM_MUTANTS, ids=[m[0] for m in ADAM_MUTANTS])
+def test_planted_adam_mistake_is_caught(name, old, new):
+    import oracle.adamw_ref
+
+    mod = _mutant(oracle.adamw_ref, old, new, name)
+    failed = []
+    for check in ADAM_CHECKS:
+        try:
+            check(mod)
+        except (AssertionError, ValueError, FloatingPointError):
+            failed.append(check.__name__)
+    assert failed, f"no pinning check caught the planted mistake {name!r}"
