@@ -432,7 +432,7 @@ def main() -> int:
         # row blocks of at most 128 rows run on the small-matrix kernels, which
         # are HBM-bound: the roofline is the dominant one, the apply of
         # X <- a·X + S·X, at 4 algorithmic bytes per element (X read once, X'
-        # written once; the Xᵀ copy it also writes is this build's layout)
+        # written once)
         ups = [r for r in recs if r["kind"] == "update"]
         um, un = units[0]
         up_ms = sum(r["ms"] for r in ups)

@@ -83,7 +83,8 @@ Plan make_plan(int64_t rows, int64_t cols, int form) {
   const size_t x = align_up((size_t)p.Mp * p.Np * 2);
   const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
   const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);
-  p.ws = 4 * x + (size_t)square_bufs(form, p.small) * a + part + kAlign;
+  // X and Xᵀ ping-pong (a small matrix keeps X only)
+  p.ws = (p.small ? 2 : 4) * x + (size_t)square_bufs(form, p.small) * a + part + kAlign;
   const double M = p.M, N = p.N;
   p.flops = M * (M + 1) * N + M * M * (M + 1) + 2 * M * M * N;
   return p;
@@ -509,8 +510,12 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
     d.X[0] = (uint16_t*)cursor; cursor += x;
     d.X[1] = (uint16_t*)cursor; cursor += x;
-    d.XT[0] = (uint16_t*)cursor; cursor += x;
-    d.XT[1] = (uint16_t*)cursor; cursor += x;
+    if (!p.small) {  // the small-matrix kernels read X transposed from LDS instead
+      d.XT[0] = (uint16_t*)cursor; cursor += x;
+      d.XT[1] = (uint16_t*)cursor; cursor += x;
+    } else {
+      d.XT[0] = d.XT[1] = nullptr;
+    }
     for (int b = 0; b < kSquareBufs; ++b) {
       d.S[b] = b < square_bufs(form, p.small) ? (uint16_t*)cursor : nullptr;
       if (b < square_bufs(form, p.small)) cursor += a;
@@ -539,7 +544,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     const MatDesc& d = items[i].desc;
     const double gb = d.g_dt == PM_DTYPE_F32 ? 4 : 2;
     const double mb = mode == MODE_STEP ? (d.m_dt == PM_DTYPE_F32 ? 8 : 4) : 0;
-    b_pro += elems * (gb + mb + 4);  // grad read, momentum read+write, X and Xᵀ bf16 writes
+    b_pro += elems * (gb + mb + (p.small ? 2 : 4));  // grad read, momentum read+write, X (and Xᵀ) bf16 writes
   }
 
   const MatDesc* ddesc = (const MatDesc*)ws;

@@ -50,7 +50,7 @@ struct MatDesc {
   float neg_lr_host;  // host-lr path: -(lr * adj_ratio), rounded once
   // workspace buffers
   uint16_t* X[2];     // bf16 Mp x Np (ld Np), ping-pong
-  uint16_t* XT[2];    // bf16 Np x Mp (ld Mp), same values transposed
+  uint16_t* XT[2];    // bf16 Np x Mp (ld Mp), same values transposed (null for small matrices)
   // bf16 Mp x Mp work matrices. Standard form: S[0] = A = X Xᵀ,
   // S[1] = B = b A + c A². Gram form: S[0] = R, S[1] = Z, S[2] = R Z + a R,
   // S[3], S[4] = Q (ping-pong). Unused entries are null.

@@ -121,10 +121,11 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
       packed[e] = (uint32_t)lo | ((uint32_t)hi << 16);
     }
     *(u32x4*)&tile[r][cg] = packed;
-    // param-layout copy: the buffer whose rows follow the param rows
+    // param-layout copy: the buffer whose rows follow the param rows (a small
+    // matrix keeps no Xᵀ: then a tall one has no param-layout copy)
     uint16_t* dst_a = d.trans ? d.XT[0] : d.X[0];
     const int64_t ld_a = d.trans ? d.Mp : d.Np;
-    *(u32x4*)(dst_a + (int64_t)pr * ld_a + pc) = packed;
+    if (dst_a) *(u32x4*)(dst_a + (int64_t)pr * ld_a + pc) = packed;
   }
   __syncthreads();
 
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
   const int64_t ld_b = d.trans ? d.Np : d.Mp;
   const int c = threadIdx.x >> 2, rb = (threadIdx.x & 3) * 16;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < 2 && dst_b; ++h) {
     u32x4 packed;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {

@@ -12,9 +12,11 @@
 //                            _gram_newtonschulz_local (pan/optim/patch_muon.py:
 //                            320-331): Z = c R² + b R; Q = a I + Z, then
 //                            Q Z + a Q; R <- Z (R Z + a R) + a (R Z + a R); S = Q
-//   pm_small_apply_kernel  X' = s·(a·X + S X) over 128-row tiles through the
-//                          grouped engine's UPDATE / FINAL epilogues (X' and
-//                          X'ᵀ, or the fused parameter step)
+//   pm_small_apply_kernel  X' = s·(a·X + S X) over 128 x 512 tiles with the
+//                          arithmetic of the grouped engine's UPDATE / FINAL
+//                          (X', or the fused parameter step). Small matrices
+//                          keep X only, no Xᵀ: the apply reads X transposed
+//                          from LDS.
 //
 // This is the counterpart of the reference's fused batched gram-NS
 // (pan/optim/muon_triton.py:234-345: the gram and the 128 x 128 iteration in
@@ -33,13 +35,10 @@ constexpr int kSmRow = kSm * 2;       // 256 B: a row of a 128 x 128 bf16 matrix
 constexpr int kSmMat = kSm * kSmRow;  // 32 KiB: one 128 x 128 bf16 matrix
 constexpr int kSmUnit = kSm * 128;    // 16 KiB: 128 rows x 64 k values, one gram unit
 constexpr int kSmRing = 8;            // gram units in LDS: 7 in flight while one is read
-#ifndef PM_SMALL_APPLY_WAVES
-#define PM_SMALL_APPLY_WAVES 8
-#endif
-constexpr int kSmApplyWaves = PM_SMALL_APPLY_WAVES;  // apply blocks: waves of 128 x 64
+constexpr int kSmApplyWaves = 8;                     // apply blocks: waves of 128 x 64
 constexpr int kSmApplyThreads = 64 * kSmApplyWaves;
-constexpr int kSmApplyCols = 64 * kSmApplyWaves;     // columns of X per apply tile
-static_assert(kSmApplyWaves == 2 || kSmApplyWaves == 4 || kSmApplyWaves == 8, "apply tile width");
+constexpr int kSmApplyCols = 64 * kSmApplyWaves;     // columns of X per apply tile: one 1 KiB row
+static_assert(kSmApplyCols * 2 == 1024, "an apply tile row is one 1 KiB copy");
 
 struct SmallCoreArgs {
   const MatDesc* descs;
@@ -347,87 +346,237 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCor
 // Chunk c16 of row r of a flat LDS array of 256-byte rows, swizzled as in SmMat.
 __device__ __forceinline__ int sm_off(int r, int c16) { return r * kSmRow + ((c16 ^ (r & 15)) << 4); }
 
+// The X tile of an apply block in LDS: kSm rows (k) of kSmApplyCols columns
+// (n), row-major as X is in HBM. Chunk c (16 B, columns 8c .. 8c+7) of row k
+// is stored at chunk c ^ (2·((k >> 3) & 3)): the transposed fragment reads
+// (16 consecutive columns of rows k, k+8, k+16, k+24 in one instruction) then
+// fall in 32 distinct banks.
+constexpr int kSmXRow = kSmApplyCols * 2;  // bytes per row of the X tile
+__device__ __forceinline__ int xt_off(int k, int n) {
+  return k * kSmXRow + ((((n >> 3) ^ (((k >> 3) & 3) << 1))) << 4) + (n & 7) * 2;
+}
+
+// Param elements r, c0 .. c0+3 of a small matrix's FINAL: whether the row is
+// in bounds, and whether the 4 elements are one aligned vector.
+struct Quad4 {
+  int r, c0;
+  bool in_row, full;
+};
+template <bool F32P>
+__device__ __forceinline__ Quad4 quad4_at(const MatDesc& d, int r, int c0) {
+  Quad4 q{r, c0, r < d.rows, false};
+  q.full = q.in_row && c0 + 3 < d.cols && (d.p_ld % 4 == 0) && ((uintptr_t)d.param % (F32P ? 16 : 8) == 0);
+  return q;
+}
+// The 4 param elements as stored (2 registers for bf16, 4 for fp32); zeros
+// outside the param.
+template <bool F32P>
+__device__ __forceinline__ typename PickVec<F32P>::type load_param4(const MatDesc& d, const Quad4& q) {
+  typedef typename PickVec<F32P>::elem E;
+  typedef typename PickVec<F32P>::type V;
+  const E* src = (const E*)d.param + (int64_t)q.r * d.p_ld + q.c0;
+  if (q.full) return *(const V*)src;
+  V v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (q.in_row && q.c0 + e < d.cols) ? src[e] : (E)0;
+  return v;
+}
+template <bool F32P>
+__device__ __forceinline__ void store_param4(const MatDesc& d, const Quad4& q, const float (&v)[4]) {
+  typedef typename PickVec<F32P>::elem E;
+  E* dst = (E*)d.param + (int64_t)q.r * d.p_ld + q.c0;
+  if (q.full) {
+    typename PickVec<F32P>::type pv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = F32P ? (E)v[e] : (E)f2bf(v[e]);
+    *(typename PickVec<F32P>::type*)dst = pv;
+  } else if (q.in_row) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (q.c0 + e < d.cols) dst[e] = F32P ? (E)v[e] : (E)f2bf(v[e]);
+  }
+}
+
 // X' = s·(a·X + S X) for one tile of kSmApplyCols columns of a small matrix
-// per block (prefix: ceil(Np / kSmApplyCols) tiles per matrix). A wide FINAL
-// computes the transposed tile X'ᵀ = Xᵀ Sᵀ (kSmApplyCols x 128; S is
-// symmetric), whose quads are param rows, as the grouped engine's FINAL does;
-// every other tile is S X. K = 128 is loaded whole into LDS. Each wave owns
-// one 128 x 64 wave tile and finishes it with the grouped engine's epilogue,
-// standing in for the engine wave at the same place in a 256 x 256 tile.
+// per block (prefix: ceil(Np / kSmApplyCols) tiles per matrix). Small
+// matrices keep X only (no Xᵀ): the X tile is copied row-major into LDS,
+// whole rows of HBM at a time, and the MFMA's B fragments (8 consecutive k
+// of one column) are read from it transposed, element by element. Each wave
+// owns a 128 x 64 wave tile. The arithmetic is the grouped engine's UPDATE /
+// FINAL (the same MFMA over the same k order, the same rounding points), so
+// the result equals the engine's on the zero-padded matrix; only the stores
+// differ: X' row-major (no Xᵀ copy), and the parameter step in param layout
+// for wide and tall matrices alike.
 template <int STAGE, int PDT>
 __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(GemmArgs args) {
-  __shared__ __attribute__((aligned(1024))) char lds[(kSm + kSmApplyCols) * kSmRow];
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) char sbuf[kSm * kSmRow];       // S, 32 KiB
+  __shared__ __attribute__((aligned(1024))) char xbuf[kSm * kSmXRow];      // X tile, 128 KiB
   const int t = blockIdx.x;
   const int m = find_matrix(args.prefix, args.n, t);
   const MatDesc& d = args.descs[m];
   const int lt = t - args.prefix[m];
   const int w = wave_id(), lane = lane_id();
-  const bool wide_final = STAGE == ST_FINAL && !d.trans;
-  // rows of S (128) and rows n0 .. n0 + kSmApplyCols - 1 of Xᵀ (ld 128), 256 B
-  // each; Xᵀ rows past Np read as zeros (buffer bounds)
+  const int Np = __builtin_amdgcn_readfirstlane(d.Np);
   const int n0 = lt * kSmApplyCols;
-  const int nx = min(kSmApplyCols, d.Np - n0);
-  const uint16_t* S = d.S[args.sl];
-  const uint16_t* XT = d.XT[args.cur] + (int64_t)n0 * kSm;
-  char* sbuf = lds;
-  char* xbuf = lds + kSm * kSmRow;
+  const int nx = min(kSmApplyCols, Np - n0);  // columns of this tile inside X
+  const uint16_t* X = d.X[args.cur];
   {
-    // copy q moves rows 4q .. 4q+3 (1 KiB): lane l lands at row 4q + l/16,
+    // S: copy q moves rows 4q .. 4q+3 (1 KiB); lane l lands at row 4q + l/16,
     // stored chunk l%16, so it loads logical chunk (l%16) ^ ((4q + l/16) & 15)
-    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(S, (uint32_t)kSm * kSmRow);
-    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(XT, (uint32_t)nx * kSmRow);
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(d.S[args.sl], (uint32_t)kSm * kSmRow);
     const int row = lane >> 4;
     for (int q = w; q < kSm / 4; q += kSmApplyWaves) {
       const int voff = row * kSmRow + (((lane & 15) ^ ((4 * q + row) & 15)) << 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(sbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
     }
-    for (int q = w; q < kSmApplyCols / 4; q += kSmApplyWaves) {
-      const int voff = row * kSmRow + (((lane & 15) ^ ((4 * q + row) & 15)) << 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
+    // X tile: copy (k, h) moves 1 KiB of row k (columns 512h .. of the tile);
+    // lane l lands at stored chunk 64h' + l, i.e. logical chunk l ^ swizzle(k)
+    // of that KiB. Columns past Np read as zeros (buffer bounds).
+    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(X + n0, (uint32_t)((kSm - 1) * Np + nx) * 2);
+    constexpr int kPerRow = kSmXRow / 1024;  // 1 KiB copies per tile row
+    for (int q = w; q < kSm * kPerRow; q += kSmApplyWaves) {
+      const int k = q / kPerRow, h = q % kPerRow;
+      const int lc = lane ^ (((k >> 3) & 3) << 1);  // logical chunk within the KiB
+      const int col = 512 * h + 8 * lc;             // first column of that chunk, tile-relative
+      const int voff = col < nx ? (k * Np + col) * 2 : 0x7fffffff;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + k * kSmXRow + h * 1024), 16, voff, 0, 0, 0);
     }
   }
   wait_vmcnt<0>();
   __syncthreads();
-  // S X: wave w owns columns n0 + 64w .. +63 (B = Xᵀ rows), all 128 rows (A = S).
-  // wide FINAL: wave w owns Xᵀ rows n0 + 128(w/2) .. +127 (A) and S rows
-  // 64(w%2) .. +63 (B).
-  const int xr = wide_final ? 128 * (w >> 1) : 64 * w;  // first Xᵀ row of the wave, tile-relative
-  if (xr >= nx) return;                                  // past Np: no barrier follows
-  const char* abuf = wide_final ? xbuf + xr * kSmRow : sbuf;
-  const char* bbuf = wide_final ? sbuf + 64 * (w & 1) * kSmRow : xbuf + xr * kSmRow;
   const int r16 = lane & 15, g = lane >> 4;
+  // the MFMA fragment of X column n for k-step s (k = 32s + 8g .. +7), read
+  // transposed from the tile, element by element
+  auto xcol = [&](int s, int n) {
+    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+    u16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = *(const uint16_t*)(xbuf + xt_off(32 * s + 8 * g + e, n));
+    return __builtin_bit_cast(bf16x8, v);
+  };
   f32x4 acc[kMi][kNi];
 #pragma unroll
   for (int i = 0; i < kMi; ++i)
 #pragma unroll
     for (int j = 0; j < kNi; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if (STAGE == ST_FINAL && !d.trans) {
+    // wide FINAL: the transposed tile X'ᵀ = Xᵀ Sᵀ, whose quads are param rows,
+    // finished by the grouped engine's FINAL epilogue. Wave w owns Xᵀ rows
+    // (columns n of X) xr .. xr+127, xr = 128(w/2), and S rows 64(w%2) .. +63.
+    const int xr = 128 * (w >> 1);
+    if (xr >= nx) return;  // past Np: no barrier follows
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8 b[kNi];
+#pragma unroll
+      for (int j = 0; j < kNi; ++j) b[j] = *(const bf16x8*)(sbuf + sm_off(64 * (w & 1) + 16 * j + r16, 4 * s + g));
+#pragma unroll
+      for (int i = 0; i < kMi; ++i) {
+        const bf16x8 a = xcol(s, xr + 16 * i + r16);
+#pragma unroll
+        for (int j = 0; j < kNi; ++j) acc[i][j] = mfma_bf16(a, b[j], acc[i][j]);
+      }
+    }
+    const int xg = n0 + xr;  // first n of the wave
+    TileJob job{};
+    job.ti = xg / kTile;
+    job.tj = 0;
+    gemm_epilogue<ST_FINAL, PDT>(args, d, job, acc, ((xg % kTile) / kWaveRows) * 4 + (w & 1));
+    return;
+  }
+  // S X: wave w owns columns xr .. xr+63 of the tile (B = X, read transposed), all 128 rows (A = S)
+  const int xr = 64 * w;
+  if (xr >= nx) return;  // past Np: no barrier follows
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     bf16x8 b[kNi];
 #pragma unroll
-    for (int j = 0; j < kNi; ++j) b[j] = *(const bf16x8*)(bbuf + sm_off(16 * j + r16, 4 * s + g));
+    for (int j = 0; j < kNi; ++j) b[j] = xcol(s, xr + 16 * j + r16);
 #pragma unroll
     for (int i = 0; i < kMi; ++i) {
-      const bf16x8 a = *(const bf16x8*)(abuf + sm_off(16 * i + r16, 4 * s + g));
+      const bf16x8 a = *(const bf16x8*)(sbuf + sm_off(16 * i + r16, 4 * s + g));
 #pragma unroll
       for (int j = 0; j < kNi; ++j) acc[i][j] = mfma_bf16(a, b[j], acc[i][j]);
     }
   }
-  // the engine wave at the same place: tile (ti, tj) of 256 x 256, wave index
-  // vw of its 2 x 4 grid of 128 x 64 wave tiles
-  const int xg = n0 + xr;  // first Xᵀ row (S X: first column) of this wave
-  TileJob job{};
-  int vw;
-  if (wide_final) {
-    job.ti = xg / kTile;
-    job.tj = 0;
-    vw = ((xg % kTile) / kWaveRows) * 4 + (w & 1);
-  } else {
-    job.ti = 0;
-    job.tj = xg / kTile;
-    vw = (xg % kTile) / kWaveCols;
+
+  // ---- epilogue: o = bf16(s·(a·X + S X)) at rows p0 .. p0+3 of column q per quad
+  const float sc = args.first ? d.scales[1] : 1.0f;
+  const float ca = args.a;
+  // the o quad of (i, j), in the accumulator layout
+  auto quad_o = [&](int i, int j, u16x4& o) {
+    const int pr = 16 * i + 4 * g + (lane & 3);
+    const int q4 = (xr + 16 * j + r16) & ~3;
+    u16x4 xq = (u16x4){0, 0, 0, 0};
+    if (ca != 0.0f)  // X[pr][q4 .. q4+3] from the tile, then to the quad layout
+      xq = quad_transpose(*(const u16x4*)(xbuf + xt_off(pr, q4)), lane);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = f2bf((ca * bf2f(xq[r]) + acc[i][j][r]) * sc);
+  };
+  if (STAGE == ST_UPDATE) {
+    uint16_t* Xn = d.X[args.cur ^ 1];
+#pragma unroll
+    for (int i = 0; i < kMi; ++i)
+#pragma unroll
+      for (int j = 0; j < kNi; ++j) {
+        u16x4 o;
+        quad_o(i, j, o);
+        const int pr = 16 * i + 4 * g + (lane & 3), q4 = (xr + 16 * j + r16) & ~3;
+        *(u16x4*)(Xn + (int64_t)pr * Np + n0 + q4) = quad_transpose(o, lane);  // row pr, columns q4 .. +3
+      }
+    return;
   }
-  gemm_epilogue<STAGE, PDT>(args, d, job, acc, vw);
+  // FINAL of a tall matrix: param row n0 + q, columns p0 .. p0+3 (o as it is;
+  // the wide branch below is never taken here, it returned above). Param loads
+  // go out kBatch rows of quads at a time, before any of them is combined.
+  constexpr bool f32p = PDT == DT_F32;
+  constexpr int kBatch = f32p ? 2 : 4;
+  const bool step = args.mode == MODE_STEP;
+  float wdf = 0.0f, neg = 0.0f;
+  if (step) {
+    if (args.lr_dev) {
+      const float lr = *args.lr_dev;
+      wdf = 1.0f - lr * args.wd;
+      neg = -(lr * d.adj_ratio);
+    } else {
+      wdf = args.wdf_host;
+      neg = d.neg_lr_host;
+    }
+  }
+  const bool wide = !d.trans;
+#pragma unroll
+  for (int i0 = 0; i0 < kMi; i0 += kBatch) {
+    __builtin_amdgcn_sched_barrier(0);
+    typename PickVec<f32p>::type pv[kBatch][kNi];
+#pragma unroll
+    for (int bi = 0; bi < kBatch; ++bi)
+#pragma unroll
+      for (int j = 0; j < kNi; ++j) {
+        const int i = i0 + bi;
+        const int p0 = 16 * i + 4 * g, pr = p0 + (lane & 3), qt = xr + 16 * j + r16;
+        const Quad4 qd = wide ? quad4_at<f32p>(d, pr, n0 + (qt & ~3)) : quad4_at<f32p>(d, n0 + qt, p0);
+        if (step) pv[bi][j] = load_param4<f32p>(d, qd);
+      }
+#pragma unroll
+    for (int bi = 0; bi < kBatch; ++bi)
+#pragma unroll
+      for (int j = 0; j < kNi; ++j) {
+        const int i = i0 + bi;
+        const int p0 = 16 * i + 4 * g, pr = p0 + (lane & 3), qt = xr + 16 * j + r16;
+        const Quad4 qd = wide ? quad4_at<f32p>(d, pr, n0 + (qt & ~3)) : quad4_at<f32p>(d, n0 + qt, p0);
+        u16x4 o;
+        quad_o(i, j, o);
+        if (wide) o = quad_transpose(o, lane);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pe = f32p ? (float)pv[bi][j][e] : bf2f((uint16_t)pv[bi][j][e]);
+          v[e] = step ? pe * wdf + bf2f(o[e]) * neg : bf2f(o[e]);
+        }
+        store_param4<f32p>(d, qd, v);
+      }
+  }
 }
 
 }  // namespace pm
