@@ -82,7 +82,7 @@ Plan make_plan(int64_t rows, int64_t cols, int form) {
   p.Np = (int32_t)round_up(p.N, kTile);
   const size_t x = align_up((size_t)p.Mp * p.Np * 2);
   const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
-  const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);
+  const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);  // (covers every run count)
   // X and Xᵀ ping-pong (a small matrix keeps X only)
   p.ws = (p.small ? 2 : 4) * x + (size_t)square_bufs(form, p.small) * a + part + kAlign;
   const double M = p.M, N = p.N;
@@ -152,7 +152,8 @@ int check_extent(int64_t rows, int64_t cols) {
 }
 
 // Work item counts of one matrix.
-int32_t pro_tiles(const Plan& p) { return (p.Mp / kProTile) * (p.Np / kProTile); }
+// Prologue blocks of one matrix (kProRun tiles each), one Σx² partial per block.
+int32_t pro_tiles(const Plan& p) { return (p.Mp / kProTile) * (p.Np / (kProTile * kProRun)); }
 int32_t sym_tiles(const Plan& p) {
   const int32_t nt = p.Mp / kTile;
   return nt * (nt + 1) / 2;

@@ -8,8 +8,8 @@ namespace pm {
 
 // ============================================================ prologue
 //
-// One 64x64 tile of the parameter per block (tiles cover the padded extent;
-// elements outside the parameter become zeros of X).
+// 64x64 tiles of the parameter, kProRun consecutive ones per block (tiles
+// cover the padded extent; elements outside the parameter become zeros of X).
 //   MODE_STEP: buf <- mu*buf + (1-mu)*g;  u <- (1-mu)*g + mu*buf  (nesterov)
 //              (pan/optim/muon_triton.py:44-48; fp32 math)
 //   MODE_NS:   u <- in
@@ -21,6 +21,8 @@ namespace pm {
 // bases allow, element by element otherwise. The copy in the other
 // orientation goes through an LDS tile.
 constexpr int kProPitch = kProTile + 8;  // LDS row pitch (elements), keeps 16-byte rows aligned
+constexpr int kProRun = 4;  // tiles per prologue block, along a tile row (1 and 2 measured slower)
+static_assert(kTile % (kProTile * kProRun) == 0, "runs tile the padded long side");
 
 __device__ __forceinline__ void load8(const void* base, int32_t dt, int64_t off, bool vec, bool in_row, int valid,
                                       float (&v)[8]) {
@@ -66,6 +68,15 @@ __device__ __forceinline__ bool vec_ok(const void* base, int32_t dt, int64_t ld)
   return (ld % 8 == 0) && ((uintptr_t)base % 16 == 0) && (dt == DT_F32 || dt == DT_BF16);
 }
 
+// A barrier that orders LDS accesses only: global loads and stores stay in
+// flight across it (__syncthreads would wait for every one of them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt unconstrained (gfx9 encoding)
+  __builtin_amdgcn_s_barrier();
+}
+
+// One block per kProRun consecutive 64x64 tiles of a tile row of X (tiles
+// cover the padded extent; elements outside the parameter become zeros of X).
 __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) uint16_t tile[kProTile][kProPitch];
@@ -75,73 +86,79 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
   const int mi = find_matrix(args.prefix, args.n, t);
   const MatDesc& d = args.descs[mi];
   const int lt = t - args.prefix[mi];
-  const int ntn = d.Np / kProTile;
-  const int ti = lt / ntn, tj = lt - ti * ntn;  // tile in X coordinates
-  const int pr0 = d.trans ? tj * kProTile : ti * kProTile;  // param-layout origin
-  const int pc0 = d.trans ? ti * kProTile : tj * kProTile;
+  const int nrun = d.Np / (kProTile * kProRun);  // runs per tile row
+  const int ti = lt / nrun, tj0 = (lt - ti * nrun) * kProRun;  // first tile in X coordinates
   const float mu = args.mu, omu = 1.0f - args.mu;
   const bool step = args.mode == MODE_STEP;
   const bool gvec = vec_ok(d.grad, d.g_dt, d.g_ld);
   const bool mvec = step && vec_ok(d.mom, d.m_dt, d.m_ld);
+  // param-layout copy: the buffer whose rows follow the param rows; the other
+  // orientation goes through the LDS tile (a small matrix keeps no Xᵀ, so one
+  // of the two is absent)
+  uint16_t* dst_a = d.trans ? d.XT[0] : d.X[0];
+  const int64_t ld_a = d.trans ? d.Mp : d.Np;
+  uint16_t* dst_b = d.trans ? d.X[0] : d.XT[0];
+  const int64_t ld_b = d.trans ? d.Np : d.Mp;
 
   float ss = 0.0f;
   const int cg = (threadIdx.x & 7) * 8;  // first column of this thread's runs
+  for (int tt = 0; tt < kProRun; ++tt) {
+    const int tj = tj0 + tt;
+    const int pr0 = d.trans ? tj * kProTile : ti * kProTile;  // param-layout origin
+    const int pc0 = d.trans ? ti * kProTile : tj * kProTile;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int r = (threadIdx.x >> 3) + 32 * h;
-    const int pr = pr0 + r, pc = pc0 + cg;
-    const bool in_row = pr < d.rows;
-    const int valid = d.cols - pc;  // elements of the run inside the parameter
-    float u[8];
-    float g[8];
-    load8(d.grad, d.g_dt, (int64_t)pr * d.g_ld + pc, gvec, in_row, valid, g);
-    if (step) {
-      float m[8];
-      const int64_t mo = (int64_t)pr * d.m_ld + pc;
-      load8(d.mom, d.m_dt, mo, mvec, in_row, valid, m);
+    for (int h = 0; h < 2; ++h) {
+      const int r = (threadIdx.x >> 3) + 32 * h;
+      const int pr = pr0 + r, pc = pc0 + cg;
+      const bool in_row = pr < d.rows;
+      const int valid = d.cols - pc;  // elements of the run inside the parameter
+      float u[8];
+      float g[8];
+      load8(d.grad, d.g_dt, (int64_t)pr * d.g_ld + pc, gvec, in_row, valid, g);
+      if (step) {
+        float m[8];
+        const int64_t mo = (int64_t)pr * d.m_ld + pc;
+        load8(d.mom, d.m_dt, mo, mvec, in_row, valid, m);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float nm = mu * m[e] + omu * g[e];
-        m[e] = nm;
-        u[e] = args.nesterov ? omu * g[e] + mu * nm : nm;
+        for (int e = 0; e < 8; ++e) {
+          const float nm = mu * m[e] + omu * g[e];
+          m[e] = nm;
+          u[e] = args.nesterov ? omu * g[e] + mu * nm : nm;
+        }
+        if (in_row) store8(d.mom, d.m_dt, mo, mvec, valid, m);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[e] = g[e];
       }
-      if (in_row) store8(d.mom, d.m_dt, mo, mvec, valid, m);
-    } else {
+      u32x4 packed;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) u[e] = g[e];
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t lo = (in_row && 2 * e < valid) ? f2bf(u[2 * e]) : (uint16_t)0;
+        const uint16_t hi = (in_row && 2 * e + 1 < valid) ? f2bf(u[2 * e + 1]) : (uint16_t)0;
+        const float flo = bf2f(lo), fhi = bf2f(hi);
+        ss += flo * flo;
+        ss += fhi * fhi;
+        packed[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+      }
+      if (dst_b) *(u32x4*)&tile[r][cg] = packed;
+      if (dst_a) *(u32x4*)(dst_a + (int64_t)pr * ld_a + pc) = packed;
     }
-    u32x4 packed;
+    if (dst_b) {
+      lds_barrier();
+      // other orientation: thread -> column c of the tile, rows 16*(t%4) .. +15
+      const int c = threadIdx.x >> 2, rb = (threadIdx.x & 3) * 16;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint16_t lo = (in_row && 2 * e < valid) ? f2bf(u[2 * e]) : (uint16_t)0;
-      const uint16_t hi = (in_row && 2 * e + 1 < valid) ? f2bf(u[2 * e + 1]) : (uint16_t)0;
-      const float flo = bf2f(lo), fhi = bf2f(hi);
-      ss += flo * flo;
-      ss += fhi * fhi;
-      packed[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+      for (int h = 0; h < 2; ++h) {
+        u32x4 packed;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb + 8 * h + 2 * e;
+          packed[e] = (uint32_t)tile[r][c] | ((uint32_t)tile[r + 1][c] << 16);
+        }
+        *(u32x4*)(dst_b + (int64_t)(pc0 + c) * ld_b + pr0 + rb + 8 * h) = packed;
+      }
+      lds_barrier();  // the tile is read before the next run overwrites it
     }
-    *(u32x4*)&tile[r][cg] = packed;
-    // param-layout copy: the buffer whose rows follow the param rows (a small
-    // matrix keeps no Xᵀ: then a tall one has no param-layout copy)
-    uint16_t* dst_a = d.trans ? d.XT[0] : d.X[0];
-    const int64_t ld_a = d.trans ? d.Mp : d.Np;
-    if (dst_a) *(u32x4*)(dst_a + (int64_t)pr * ld_a + pc) = packed;
-  }
-  __syncthreads();
-
-  // other orientation: thread -> column c of the tile, rows 16*(t%4) .. +15
-  uint16_t* dst_b = d.trans ? d.X[0] : d.XT[0];
-  const int64_t ld_b = d.trans ? d.Np : d.Mp;
-  const int c = threadIdx.x >> 2, rb = (threadIdx.x & 3) * 16;
-#pragma unroll
-  for (int h = 0; h < 2 && dst_b; ++h) {
-    u32x4 packed;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = rb + 8 * h + 2 * e;
-      packed[e] = (uint32_t)tile[r][c] | ((uint32_t)tile[r + 1][c] << 16);
-    }
-    *(u32x4*)(dst_b + (int64_t)(pc0 + c) * ld_b + pr0 + rb + 8 * h) = packed;
   }
 
   ss = wave_sum(ss);
