@@ -483,8 +483,9 @@ def main() -> int:
             "kind": "reference",
             "sample": ("stock torch.optim.Muon step (the reference's float-lr path, pan/optim/muon.py:126-154), "
                        f"fp32, one matrix per distinct shape ({', '.join(cb['timed_shapes'])}) timed on "
-                       f"{cb['cores']} host threads; " + ("extrapolated to the config's counts by shape"
-                                                          if cb["extrapolated"] else "full config")),
+                       f"{cb['cores']} host threads (short steps: median of 3 or 5 after a warm-up; "
+                       f"repeats {cb['repeats']}); " + ("extrapolated to the config's counts by shape"
+                                                        if cb["extrapolated"] else "full config")),
             "cpu": cb["cpu"],
         }
 

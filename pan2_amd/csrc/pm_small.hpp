@@ -527,9 +527,9 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
       }
     return;
   }
-  // FINAL of a tall matrix: param row n0 + q, columns p0 .. p0+3 (o as it is;
-  // the wide branch below is never taken here, it returned above). Param loads
-  // go out kBatch rows of quads at a time, before any of them is combined.
+  // FINAL of a tall matrix (a wide one returned above): param row n0 + q,
+  // columns p0 .. p0+3, o as it is. Param loads go out kBatch rows of quads
+  // at a time, before any of them is combined.
   constexpr bool f32p = PDT == DT_F32;
   constexpr int kBatch = f32p ? 2 : 4;
   const bool step = args.mode == MODE_STEP;
@@ -544,7 +544,6 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
       neg = d.neg_lr_host;
     }
   }
-  const bool wide = !d.trans;
 #pragma unroll
   for (int i0 = 0; i0 < kMi; i0 += kBatch) {
     __builtin_amdgcn_sched_barrier(0);
@@ -553,21 +552,16 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
     for (int bi = 0; bi < kBatch; ++bi)
 #pragma unroll
       for (int j = 0; j < kNi; ++j) {
-        const int i = i0 + bi;
-        const int p0 = 16 * i + 4 * g, pr = p0 + (lane & 3), qt = xr + 16 * j + r16;
-        const Quad4 qd = wide ? quad4_at<f32p>(d, pr, n0 + (qt & ~3)) : quad4_at<f32p>(d, n0 + qt, p0);
+        const Quad4 qd = quad4_at<f32p>(d, n0 + xr + 16 * j + r16, 16 * (i0 + bi) + 4 * g);
         if (step) pv[bi][j] = load_param4<f32p>(d, qd);
       }
 #pragma unroll
     for (int bi = 0; bi < kBatch; ++bi)
 #pragma unroll
       for (int j = 0; j < kNi; ++j) {
-        const int i = i0 + bi;
-        const int p0 = 16 * i + 4 * g, pr = p0 + (lane & 3), qt = xr + 16 * j + r16;
-        const Quad4 qd = wide ? quad4_at<f32p>(d, pr, n0 + (qt & ~3)) : quad4_at<f32p>(d, n0 + qt, p0);
+        const Quad4 qd = quad4_at<f32p>(d, n0 + xr + 16 * j + r16, 16 * (i0 + bi) + 4 * g);
         u16x4 o;
-        quad_o(i, j, o);
-        if (wide) o = quad_transpose(o, lane);
+        quad_o(i0 + bi, j, o);
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
