@@ -105,3 +105,22 @@ def test_full_size_chunked_qkv_weight():
         assert rel_fro(out[i].float(), ref[i]) <= 2e-2, i
     s = singular_values(out.float()).cpu().numpy()
     assert lo - 0.03 <= s.min() and s.max() <= hi + 0.03, (s.min(), s.max(), lo, hi)
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 1 << 22), ((1 << 22) + 256, 100), (256, 1 << 21)])
+def test_long_side_near_the_offset_limits(rows, cols):
+    """Long sides of millions of elements: the 32-bit buffer offsets of the
+    small-matrix kernels (128 rows of X) and of the engine's 256-row panels stay
+    inside their ranges; the result keeps the fp32 gate and the band."""
+    print(f"long-side ns {rows}x{cols}", flush=True)
+    g = gaussian((rows, cols), 99 + rows + cols)
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV)
+    _lib.newton_schulz_into([(g, out)])
+    ref = ns_fp32(g)
+    err = rel_fro(out.float(), ref)
+    s = singular_values(out.float()).cpu().numpy()
+    lo, hi = band(rows, cols)
+    print(f"  rel-Frobenius vs fp32 {err:.4f}; singular values [{s.min():.4f}, {s.max():.4f}] in [{lo:.4f}, {hi:.4f}]",
+          flush=True)
+    assert err <= 2e-2
+    assert lo - 0.03 <= s.min() and s.max() <= hi + 0.03
