@@ -213,6 +213,40 @@ def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
     return 0
 
 
+def hbm_stream(device, mib: int = 2048, reps: int = 5) -> dict:
+    """What plain streams reach on this box's HBM, beside the 8 TB/s peak the
+    HBM rooflines are quoted against: torch's device copy (mib MiB read + mib
+    written), a fill (written) and a sum (read), best of reps, by HIP events on
+    the current stream. Run after the timed region."""
+    import torch
+
+    n = (mib << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+
+    def best(fn):
+        fn()
+        ms = []
+        for _ in range(reps):
+            ev[0].record()
+            fn()
+            ev[1].record()
+            ev[1].synchronize()
+            ms.append(ev[0].elapsed_time(ev[1]))
+        return min(ms)
+
+    nbytes = n * 4
+    out = {
+        "copy_gbs": round(2 * nbytes / (best(lambda: dst.copy_(src)) * 1e-3) / 1e9, 1),
+        "write_gbs": round(nbytes / (best(lambda: dst.fill_(2.0)) * 1e-3) / 1e9, 1),
+        "read_gbs": round(nbytes / (best(lambda: src.sum()) * 1e-3) / 1e9, 1),
+        "mib": mib,
+    }
+    del src, dst
+    return out
+
+
 def bench_adamw(args) -> int:
     """One AdamW.step() over PAN 2's AdamW param set (fp32 params, grads and
     state, tensor lr): libpanmuon's pm_adam_step behind torch's fused AdamW,
@@ -277,6 +311,7 @@ def bench_adamw(args) -> int:
         pa._adam_module._fused_adam = stock
     kern_ms = sum(r["ms"] for r in recs) / max(1, len(recs))
     achieved = bytes_per_step / (kern_ms * 1e-3) / 1e9 if kern_ms > 0 else 0.0
+    stream = hbm_stream(device)
     cpu = None
     if not args.no_cpu_baseline:
         # torch's CPU AdamW (foreach) over the same set, one timed step after one warmup
@@ -319,6 +354,7 @@ def bench_adamw(args) -> int:
         "roofline": {"kernel": "pm_adam_kernel", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": None, "avg_launch_ms": round(kern_ms, 4)},
+        "hbm_stream": stream,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
@@ -406,6 +442,7 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     recs = _lib.timing_read()
     _lib.timing_enable(False)
+    stream = hbm_stream(device)
     if args.copy_mib:
         # HBM counter calibration: a copy kernel that reads and writes exactly copy_mib MiB
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device)
@@ -520,6 +557,7 @@ def main() -> int:
         "pct_peak_step": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "host_ms_per_step": round(host * 1e3 / args.steps, 3),
         "roofline": roofline,
+        "hbm_stream": stream,
         "stages": stages,
         "cpu_baseline": cpu,
     }

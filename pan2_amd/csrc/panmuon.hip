@@ -318,7 +318,7 @@ struct Launcher {
     a.stage = ST_GRAM; a.cur = cur; a.first = first; a.sc = sc;
     a.prefix = sym; a.total = sym_total;
     if (int rc = next_queues(a)) return rc;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
+    hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_GRAM, DT_BF16, kWsLayout>), dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
     timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
     return check("gram launch");
   }
@@ -328,7 +328,7 @@ struct Launcher {
     a.stage = ST_SYMM; a.sl = sl; a.sr = sr; a.sd = sd; a.sc = sc; a.c = alpha; a.b = beta;
     a.prefix = sym; a.total = sym_total;
     if (int rc = next_queues(a)) return rc;
-    hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_SYMM>, dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
+    hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_SYMM, DT_BF16, kWsLayout>), dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
     timing_mark(stream, PM_K_POLY, group, it, count, f_sym, 0.0);
     return check("symmetric product launch");
   }
@@ -339,11 +339,11 @@ struct Launcher {
     a.prefix = full; a.total = full_total;
     if (int rc = next_queues(a)) return rc;
     if (last && final_f32)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32, kWsLayout>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
     else if (last)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16, kWsLayout>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_UPDATE>, dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_UPDATE, DT_BF16, kWsLayout>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
     timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
     return check("Newton-Schulz update launch");
   }
@@ -375,7 +375,7 @@ struct Launcher {
   int qinit(int sz, int sq, float coef_a, int max_mp, int it) {
     for (int first = 0; first < count; first += 65535)  // gridDim.y limit
       hipLaunchKernelGGL(pm_qinit_kernel, dim3(max_mp / kProTile, std::min(count - first, 65535)), dim3(kThreads), 0,
-                         stream, ga.descs, first, sz, sq, coef_a);
+                         stream, ga.descs, first, sz, sq, coef_a, (int32_t)((kWsLayout & kTiledS) != 0));
     timing_mark(stream, PM_K_QINIT, group, it, count, 0.0, 0.0);
     return check("Q init launch");
   }
@@ -554,7 +554,12 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   const int32_t* dfull = (const int32_t*)(ws + ((char*)full - host.data()));
   int32_t* dqueues = (int32_t*)(ws + ((const char*)queues - host.data()));
 
-  ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov};
+  // run_all keeps small and engine matrices in separate groups: the engine's
+  // workspace matrices are in the panel layout, small matrices' X row-major
+  const bool small = items[0].plan.small;
+  for (int i = 1; i < count; ++i)
+    if (items[i].plan.small != small) return fail(PM_EINVAL, "internal: a group mixes small and large matrices");
+  ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov, (small || !(kWsLayout & kTiledX)) ? 0 : 1, 0};
   hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
   timing_mark(stream, PM_K_PROLOGUE, group, -1, count, 0.0, b_pro);
   hipLaunchKernelGGL(pm_norm_kernel, dim3(count), dim3(kThreads), 0, stream, ddesc, hp->eps);
@@ -847,7 +852,7 @@ int pm_gram(const void* x, int64_t rows, int64_t cols, void* out, void* workspac
   ga.cur = 0;
   ga.first = 0;
   ga.sc = 0;
-  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_GRAM>, dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
+  hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_GRAM, DT_BF16, 0>), dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PM_OK : hip_fail(e, "gram launch");
 }
@@ -893,7 +898,7 @@ int pm_gemm_symmetric(const void* left, const void* right, const void* addend, v
   ga.sc = 3;
   ga.c = alpha;
   ga.b = beta;
-  hipLaunchKernelGGL(pm_ns_gemm_kernel<ST_SYMM>, dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
+  hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_SYMM, DT_BF16, 0>), dim3(gemm_grid(sym[1])), dim3(kGemmThreads), 0, s, ga);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PM_OK : hip_fail(e, "symmetric product launch");
 }

@@ -49,6 +49,8 @@ struct MatDesc {
   float adj_ratio;    // device-lr path: adjusted_lr = lr * adj_ratio
   float neg_lr_host;  // host-lr path: -(lr * adj_ratio), rounded once
   // workspace buffers
+  // X, Xᵀ and S are in the panel layout of ws_off for large matrices,
+  // row-major for small ones (Mp = 128)
   uint16_t* X[2];     // bf16 Mp x Np (ld Np), ping-pong
   uint16_t* XT[2];    // bf16 Np x Mp (ld Mp), same values transposed (null for small matrices)
   // bf16 Mp x Mp work matrices. Standard form: S[0] = A = X Xᵀ,
@@ -68,6 +70,8 @@ struct ProArgs {
   int32_t mode;
   float mu;
   int32_t nesterov;
+  int32_t tiled;          // X / Xᵀ in the panel layout (ws_off); 0: row-major (small matrices)
+  int32_t pad_;
 };
 
 struct GemmArgs {
@@ -87,7 +91,30 @@ struct GemmArgs {
   float wdf_host;         // 1 - lr*wd (host-lr path)
 };
 
+// Layouts of the GEMM engine's operands and outputs (a template parameter of
+// pm_ns_gemm_kernel): bits set for the matrices kept in the panel layout of
+// ws_off, the rest row-major. The grouped Muon / Newton–Schulz path keeps all
+// of them in the panel layout; pm_gram and pm_gemm_symmetric take the caller's
+// row-major matrices.
+constexpr int kTiledX = 1;  // X and Xᵀ
+constexpr int kTiledS = 2;  // the Mp x Mp work matrices
+constexpr int kWsLayout = kTiledX | kTiledS;
+
 // ---------------------------------------------------------------- helpers
+
+// Element offset of (r, c) in a workspace matrix with ld columns.
+// Row-major: r·ld + c. Panel layout (tiled): the matrix is cut into panels of
+// kTile rows and each panel into units of 64 columns; unit (r/256, c/64) is a
+// contiguous 32 KiB block of 256 rows of 128 bytes. A panel starts where it
+// does row-major (row 256·i), and one unit of a panel is exactly what the GEMM
+// engine streams into LDS per K step, so each of its 1 KiB copies (8 rows) reads
+// contiguous memory. Needs ld a multiple of 64 and rows a multiple of 256 (the
+// engine's padded extents). Runs of up to 8 elements starting at a multiple of
+// their length stay contiguous in both layouts.
+__device__ __forceinline__ int64_t ws_off(int r, int c, int64_t ld, bool tiled) {
+  if (!tiled) return (int64_t)r * ld + c;
+  return ((((int64_t)(r >> 8) * (ld >> 6)) + (c >> 6)) << 14) + ((r & 255) << 6) + (c & 63);
+}
 
 __device__ __forceinline__ uint16_t f2bf(float f) {
   __bf16 h = (__bf16)f;  // v_cvt_pk_bf16_f32: round to nearest even, NaN kept

@@ -482,7 +482,7 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
     TileJob job{};
     job.ti = xg / kTile;
     job.tj = 0;
-    gemm_epilogue<ST_FINAL, PDT>(args, d, job, acc, ((xg % kTile) / kWaveRows) * 4 + (w & 1));
+    gemm_epilogue<ST_FINAL, PDT, 0>(args, d, job, acc, ((xg % kTile) / kWaveRows) * 4 + (w & 1));  // X row-major
     return;
   }
   // S X: wave w owns columns xr .. xr+63 of the tile (B = X, read transposed), all 128 rows (A = S)

@@ -36,7 +36,8 @@ def gemm_kernels(tmp_path_factory):
     for m in re.finditer(r"^(_ZN2pm17pm_ns_gemm_kernel\w+):.*$", asm, flags=re.M):
         body = asm[m.end():]
         kernels[m.group(1)] = body[:body.index("s_endpgm")].split("\n")
-    assert len(kernels) == 5, sorted(kernels)  # GRAM, POLY, UPDATE, FINAL x {f32, bf16}
+    # panel layout: GRAM, POLY, UPDATE, FINAL x {f32, bf16}; row-major: GRAM, POLY (pm_gram, pm_gemm_symmetric)
+    assert len(kernels) == 7, sorted(kernels)
     return kernels
 
 
