@@ -154,9 +154,10 @@ def traffic_summary(args) -> int:
     result = {}
     for counter, path in (("FETCH_SIZE", args.fetch_csv), ("WRITE_SIZE", args.write_csv)):
         vals = _counter_by_dispatch(path, counter)
-        # the calibration copies are the large copy dispatches (the counter may
-        # read a fixed fraction of the bytes: that fraction is the scale)
-        copies = [v for (d, k), v in vals.items() if COPY_KERNEL in k and v >= 0.25 * known_kib]
+        # the calibration copies are the last three copy dispatches of the run
+        # (the counter may read a fixed fraction of the bytes: that fraction is
+        # the scale)
+        copies = [v for (d, k), v in sorted(vals.items(), key=lambda kv: int(kv[0][0])) if COPY_KERNEL in k][-3:]
         gemm = [v for (d, k), v in vals.items() if GEMM_KERNEL in k]
         if not copies or not gemm:
             print(f"{counter}: no calibration copy or no GEMM dispatches in {path}", file=sys.stderr)
@@ -216,8 +217,8 @@ def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
 def hbm_stream(device, mib: int = 2048, reps: int = 5) -> dict:
     """What plain streams reach on this box's HBM, beside the 8 TB/s peak the
     HBM rooflines are quoted against: torch's device copy (mib MiB read + mib
-    written), a fill (written) and a sum (read), best of reps, by HIP events on
-    the current stream. Run after the timed region."""
+    written) and a fill (mib MiB written), best of reps, by HIP events on the
+    current stream. Run after the timed region."""
     import torch
 
     n = (mib << 20) // 4
@@ -240,7 +241,6 @@ def hbm_stream(device, mib: int = 2048, reps: int = 5) -> dict:
     out = {
         "copy_gbs": round(2 * nbytes / (best(lambda: dst.copy_(src)) * 1e-3) / 1e9, 1),
         "write_gbs": round(nbytes / (best(lambda: dst.fill_(2.0)) * 1e-3) / 1e9, 1),
-        "read_gbs": round(nbytes / (best(lambda: src.sum()) * 1e-3) / 1e9, 1),
         "mib": mib,
     }
     del src, dst
@@ -442,7 +442,8 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     recs = _lib.timing_read()
     _lib.timing_enable(False)
-    stream = hbm_stream(device)
+    # (not in counter runs: its copies would join the calibration copies)
+    stream = None if args.copy_mib else hbm_stream(device)
     if args.copy_mib:
         # HBM counter calibration: a copy kernel that reads and writes exactly copy_mib MiB
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device)
