@@ -682,7 +682,9 @@ __device__ __forceinline__ int xcc_id() {
 // to bf16 where torch rounds it.
 // PDT is the param dtype of the FINAL epilogue (one instantiation per dtype
 // keeps the epilogue's registers within budget); other stages ignore it.
-template <int STAGE, int PDT, int LAYOUT, class D>
+// AX_IN_ACC (FINAL): the caller has already added a·X to the accumulators
+// (acc = a·x + acc, the same fp32 operations), so X is not read again.
+template <int STAGE, int PDT, int LAYOUT, bool AX_IN_ACC = false, class D>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, const TileJob& job,
                                               const f32x4 (&acc)[kMi][kNi], int wave) {
 #pragma clang fp contract(off)
@@ -826,7 +828,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
       for (int j = 0; j < kNi; ++j) {
         const int c0 = pbase + (b0 + bi) * 16, r = qbase + j * 16;  // param row r, columns c0..c0+3
-        xv[bi][j] = (ca != 0.0f) ? *(const u16x4*)(T + ws_off(r, c0, ldt, tx)) : (u16x4){0, 0, 0, 0};
+        xv[bi][j] = (!AX_IN_ACC && ca != 0.0f) ? *(const u16x4*)(T + ws_off(r, c0, ldt, tx)) : (u16x4){0, 0, 0, 0};
         if (!step) continue;
         const bool in_row = r < prow;
         typedef typename PickVec<f32p>::elem E;
@@ -848,7 +850,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float on = bf2f(f2bf((ca * bf2f(xv[bi][j][e]) + acc[mi][j][e]) * s));  // bf16 orthogonalised update
+          // bf16 orthogonalised update
+          const float on = AX_IN_ACC ? bf2f(f2bf(acc[mi][j][e] * s))
+                                     : bf2f(f2bf((ca * bf2f(xv[bi][j][e]) + acc[mi][j][e]) * s));
           const float pe = f32p ? (float)pv[bi][j][e] : bf2f((uint16_t)pv[bi][j][e]);
           o[e] = step ? pe * wdf + on * neg : on;
         }

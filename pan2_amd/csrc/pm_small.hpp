@@ -482,7 +482,25 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
     TileJob job{};
     job.ti = xg / kTile;
     job.tj = 0;
-    gemm_epilogue<ST_FINAL, PDT, 0>(args, d, job, acc, ((xg % kTile) / kWaveRows) * 4 + (w & 1));  // X row-major
+    const int ew = ((xg % kTile) / kWaveRows) * 4 + (w & 1);  // the engine wave whose quads these are
+    if (args.a != 0.0f) {
+      // a·X from the tile in LDS rather than from HBM: quad (i, j) is
+      // Xᵀ[xr + 16i + 4g .. +3][m], m = 64(w%2) + 16j + lane%16, i.e. 4
+      // consecutive columns of X row m; acc = a·x + acc as the engine's epilogue
+      // forms it
+      const float ca = args.a;
+#pragma unroll
+      for (int i = 0; i < kMi; ++i)
+#pragma unroll
+        for (int j = 0; j < kNi; ++j) {
+          const u16x4 xq = *(const u16x4*)(xbuf + xt_off(64 * (w & 1) + 16 * j + r16, xr + 16 * i + 4 * g));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = ca * bf2f(xq[r]) + acc[i][j][r];
+        }
+      gemm_epilogue<ST_FINAL, PDT, 0, true>(args, d, job, acc, ew);  // X row-major
+    } else {
+      gemm_epilogue<ST_FINAL, PDT, 0>(args, d, job, acc, ew);
+    }
     return;
   }
   // S X: wave w owns columns xr .. xr+63 of the tile (B = X, read transposed), all 128 rows (A = S)
