@@ -70,7 +70,7 @@ struct ProArgs {
   int32_t mode;
   float mu;
   int32_t nesterov;
-  int32_t tiled;          // X / Xᵀ in the panel layout (ws_off); 0: row-major (small matrices)
+  int32_t layout;         // of X / Xᵀ: 0 row-major, 1 the panel layout (ws_off), 2 small X (sm_x_off)
   int32_t pad_;
 };
 
@@ -114,6 +114,12 @@ constexpr int kWsLayout = kTiledX | kTiledS;
 __device__ __forceinline__ int64_t ws_off(int r, int c, int64_t ld, bool tiled) {
   if (!tiled) return (int64_t)r * ld + c;
   return ((((int64_t)(r >> 8) * (ld >> 6)) + (c >> 6)) << 14) + ((r & 255) << 6) + (c & 63);
+}
+
+// The same layout for a small matrix's X (128 x Np, one panel of 128 rows):
+// unit c/64 is a contiguous 16 KiB block of 128 rows of 128 bytes.
+__device__ __forceinline__ int64_t sm_x_off(int r, int c) {
+  return ((int64_t)(c >> 6) << 13) + (r << 6) + (c & 63);
 }
 
 __device__ __forceinline__ uint16_t f2bf(float f) {

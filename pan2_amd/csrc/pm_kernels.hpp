@@ -99,7 +99,8 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
   const int64_t ld_a = d.trans ? d.Mp : d.Np;
   uint16_t* dst_b = d.trans ? d.X[0] : d.XT[0];
   const int64_t ld_b = d.trans ? d.Np : d.Mp;
-  const bool tiled = args.tiled;
+  const int layout = args.layout;
+  auto x_off = [&](int r, int c, int64_t ld) { return layout == 2 ? sm_x_off(r, c) : ws_off(r, c, ld, layout == 1); };
 
   float ss = 0.0f;
   const int cg = (threadIdx.x & 7) * 8;  // first column of this thread's runs
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
         packed[e] = (uint32_t)lo | ((uint32_t)hi << 16);
       }
       if (dst_b) *(u32x4*)&tile[r][cg] = packed;
-      if (dst_a) *(u32x4*)(dst_a + ws_off(pr, pc, ld_a, tiled)) = packed;
+      if (dst_a) *(u32x4*)(dst_a + x_off(pr, pc, ld_a)) = packed;
     }
     if (dst_b) {
       lds_barrier();
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
           const int r = rb + 8 * h + 2 * e;
           packed[e] = (uint32_t)tile[r][c] | ((uint32_t)tile[r + 1][c] << 16);
         }
-        *(u32x4*)(dst_b + ws_off(pc0 + c, pr0 + rb + 8 * h, ld_b, tiled)) = packed;
+        *(u32x4*)(dst_b + x_off(pc0 + c, pr0 + rb + 8 * h, ld_b)) = packed;
       }
       lds_barrier();  // the tile is read before the next run overwrites it
     }

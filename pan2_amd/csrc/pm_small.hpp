@@ -199,20 +199,20 @@ struct SmRing {
   char* s[kSmRing];
 };
 
-// Unit u of the gram, 64 k values: rows 0..127, bytes 128u .. 128u+127 of each
-// row of X (ld Np), 16 copies of 1 KiB (8 rows); wave w issues copies 2w and
-// 2w+1. Chunk c of row r is stored at chunk c ^ ((r >> 1) & 7), as in the
-// grouped engine.
+// Unit u of the gram, 64 k values: rows 0..127 of columns 64u .. 64u+63 of X,
+// one contiguous 16 KiB block in the panel layout (sm_x_off); 16 copies of
+// 1 KiB (8 rows); wave w issues copies 2w and 2w+1. Chunk c of row r is stored
+// at chunk c ^ ((r >> 1) & 7), as in the grouped engine.
 struct SmCopy {
   __amdgpu_buffer_rsrc_t rsrc;
   int voff[2];  // lane offsets of copies 2w, 2w+1
-  int row8;     // bytes of 8 rows of X
   int wave;
   __device__ __forceinline__ void operator()(char* dst, int u) const {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int q = 2 * wave + h;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to_lds(dst + q * 1024), 16, voff[h], q * row8 + u * 128, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to_lds(dst + q * 1024), 16, voff[h], u * kSmUnit + q * 1024, 0,
+                                               0);
     }
   }
 };
@@ -270,13 +270,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCor
   const int K = __builtin_amdgcn_readfirstlane(d.Np), KT = K / 64;
   SmCopy copy;
   copy.rsrc = uniform_rsrc(d.X[args.cur], (uint32_t)kSm * K * 2);
-  copy.row8 = 8 * K * 2;
   copy.wave = wave;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {  // copy q = 2w + h: row 8q + lane/8, stored chunk lane%8
     const int q = 2 * wave + h;
     const int sw = (4 * (q & 1) + (lane >> 4)) & 7;  // ((8q + lane/8) >> 1) & 7
-    copy.voff[h] = (lane >> 3) * K * 2 + (((lane & 7) ^ sw) << 4);
+    copy.voff[h] = (lane >> 3) * 128 + (((lane & 7) ^ sw) << 4);
   }
   f32x4 acc[4][2];
 #pragma unroll
@@ -346,14 +345,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCor
 // Chunk c16 of row r of a flat LDS array of 256-byte rows, swizzled as in SmMat.
 __device__ __forceinline__ int sm_off(int r, int c16) { return r * kSmRow + ((c16 ^ (r & 15)) << 4); }
 
-// The X tile of an apply block in LDS: kSm rows (k) of kSmApplyCols columns
-// (n), row-major as X is in HBM. Chunk c (16 B, columns 8c .. 8c+7) of row k
-// is stored at chunk c ^ (2·((k >> 3) & 3)): the transposed fragment reads
-// (16 consecutive columns of rows k, k+8, k+16, k+24 in one instruction) then
-// fall in 32 distinct banks.
-constexpr int kSmXRow = kSmApplyCols * 2;  // bytes per row of the X tile
+// The X tile of an apply block in LDS, laid out as X is in HBM (sm_x_off):
+// kSmApplyCols / 64 units of 64 columns (n), each kSm rows (k) of 128 B.
+// Chunk c (16 B, columns 8c .. 8c+7 of the unit) of row k is stored at chunk
+// c ^ (2·((k >> 3) & 3)): the transposed fragment reads (16 consecutive
+// columns of rows k, k+8, k+16, k+24 in one instruction) then fall in 32
+// distinct banks.
+constexpr int kSmXUnits = kSmApplyCols / 64;  // units per tile
 __device__ __forceinline__ int xt_off(int k, int n) {
-  return k * kSmXRow + ((((n >> 3) ^ (((k >> 3) & 3) << 1))) << 4) + (n & 7) * 2;
+  return (n >> 6) * kSmUnit + k * 128 + ((((n >> 3) & 7) ^ (((k >> 3) & 3) << 1)) << 4) + (n & 7) * 2;
 }
 
 // Param elements r, c0 .. c0+3 of a small matrix's FINAL: whether the row is
@@ -399,19 +399,19 @@ __device__ __forceinline__ void store_param4(const MatDesc& d, const Quad4& q, c
 
 // X' = s·(a·X + S X) for one tile of kSmApplyCols columns of a small matrix
 // per block (prefix: ceil(Np / kSmApplyCols) tiles per matrix). Small
-// matrices keep X only (no Xᵀ): the X tile is copied row-major into LDS,
-// whole rows of HBM at a time, and the MFMA's B fragments (8 consecutive k
-// of one column) are read from it transposed, element by element. Each wave
-// owns a 128 x 64 wave tile. The arithmetic is the grouped engine's UPDATE /
-// FINAL (the same MFMA over the same k order, the same rounding points), so
-// the result equals the engine's on the zero-padded matrix; only the stores
-// differ: X' row-major (no Xᵀ copy), and the parameter step in param layout
-// for wide and tall matrices alike.
+// matrices keep X only (no Xᵀ): the X tile, 128 contiguous KiB of HBM in the
+// panel layout (sm_x_off), is copied into LDS in that layout, and the MFMA's
+// B fragments (8 consecutive k of one column) are read from it transposed,
+// element by element. Each wave owns a 128 x 64 wave tile. The arithmetic is
+// the grouped engine's UPDATE / FINAL (the same MFMA over the same k order,
+// the same rounding points), so the result equals the engine's on the
+// zero-padded matrix; only the stores differ: X' alone (no Xᵀ copy), and the
+// parameter step in param layout for wide and tall matrices alike.
 template <int STAGE, int PDT>
 __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(1024))) char sbuf[kSm * kSmRow];       // S, 32 KiB
-  __shared__ __attribute__((aligned(1024))) char xbuf[kSm * kSmXRow];      // X tile, 128 KiB
+  __shared__ __attribute__((aligned(1024))) char xbuf[kSmXUnits * kSmUnit];  // X tile, 128 KiB
   const int t = blockIdx.x;
   const int m = find_matrix(args.prefix, args.n, t);
   const MatDesc& d = args.descs[m];
@@ -430,17 +430,17 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
       const int voff = row * kSmRow + (((lane & 15) ^ ((4 * q + row) & 15)) << 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(sbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
     }
-    // X tile: copy (k, h) moves 1 KiB of row k (columns 512h .. of the tile);
-    // lane l lands at stored chunk 64h' + l, i.e. logical chunk l ^ swizzle(k)
-    // of that KiB. Columns past Np read as zeros (buffer bounds).
-    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(X + n0, (uint32_t)((kSm - 1) * Np + nx) * 2);
-    constexpr int kPerRow = kSmXRow / 1024;  // 1 KiB copies per tile row
-    for (int q = w; q < kSm * kPerRow; q += kSmApplyWaves) {
-      const int k = q / kPerRow, h = q % kPerRow;
-      const int lc = lane ^ (((k >> 3) & 3) << 1);  // logical chunk within the KiB
-      const int col = 512 * h + 8 * lc;             // first column of that chunk, tile-relative
-      const int voff = col < nx ? (k * Np + col) * 2 : 0x7fffffff;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + k * kSmXRow + h * 1024), 16, voff, 0, 0, 0);
+    // X tile: the tile's units are contiguous in HBM (sm_x_off; n0 is a
+    // multiple of 64). Copy q moves rows 8(q%16) .. +7 of unit q/16 (1 KiB);
+    // lane l lands at row 8(q%16) + l/8, stored chunk l%8, so it loads logical
+    // chunk (l%8) ^ swizzle(row). Units past Np read as zeros (buffer bounds).
+    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(X + sm_x_off(0, n0), (uint32_t)(nx / 64) * kSmUnit);
+    for (int q = w; q < kSmXUnits * (kSm / 8); q += kSmApplyWaves) {
+      const int j = q / (kSm / 8), k = 8 * (q % (kSm / 8)) + (lane >> 3);
+      const int lc = (lane & 7) ^ (((k >> 3) & 3) << 1);  // logical chunk of row k
+      const int voff = 64 * j < nx ? j * kSmUnit + k * 128 + lc * 16 : 0x7fffffff;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + j * kSmUnit + (q % (kSm / 8)) * 1024), 16, voff, 0,
+                                               0, 0);
     }
   }
   wait_vmcnt<0>();
@@ -497,9 +497,9 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[i][j][r] = ca * bf2f(xq[r]) + acc[i][j][r];
         }
-      gemm_epilogue<ST_FINAL, PDT, 0, true>(args, d, job, acc, ew);  // X row-major
+      gemm_epilogue<ST_FINAL, PDT, 0, true>(args, d, job, acc, ew);
     } else {
-      gemm_epilogue<ST_FINAL, PDT, 0>(args, d, job, acc, ew);
+      gemm_epilogue<ST_FINAL, PDT, 0>(args, d, job, acc, ew);  // a = 0: X is not read
     }
     return;
   }
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
         u16x4 o;
         quad_o(i, j, o);
         const int pr = 16 * i + 4 * g + (lane & 3), q4 = (xr + 16 * j + r16) & ~3;
-        *(u16x4*)(Xn + (int64_t)pr * Np + n0 + q4) = quad_transpose(o, lane);  // row pr, columns q4 .. +3
+        *(u16x4*)(Xn + sm_x_off(pr, n0 + q4)) = quad_transpose(o, lane);  // row pr, columns q4 .. +3
       }
     return;
   }
