@@ -352,7 +352,10 @@ struct Launcher {
   const float* coeffs = nullptr;  // device (a, b, c) per iteration
   int small_core(int cur, bool first, int it0, int steps, int it) {
     const SmallCoreArgs a{ga.descs, coeffs, it0, steps, cur, first, 0, 0};
-    hipLaunchKernelGGL(pm_small_core_kernel, dim3(count), dim3(kGemmThreads), 0, stream, a);
+    if (steps == 0)  // the standard form's M x M part fits a 4-slot ring: two blocks per CU
+      hipLaunchKernelGGL(pm_small_core_kernel<kSmRingStd>, dim3(count), dim3(kGemmThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL(pm_small_core_kernel<kSmRing>, dim3(count), dim3(kGemmThreads), 0, stream, a);
     const int products = steps == 0 ? 1 : 4 * steps - 3;
     timing_mark(stream, PM_K_SMALL_CORE, group, it, count, f_gram + products * f_sym, 0.0);
     return check("small-matrix core launch");

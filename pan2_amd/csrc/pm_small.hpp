@@ -34,7 +34,8 @@ constexpr int kSm = 128;              // padded short side of a small matrix
 constexpr int kSmRow = kSm * 2;       // 256 B: a row of a 128 x 128 bf16 matrix, or 128 k values
 constexpr int kSmMat = kSm * kSmRow;  // 32 KiB: one 128 x 128 bf16 matrix
 constexpr int kSmUnit = kSm * 128;    // 16 KiB: 128 rows x 64 k values, one gram unit
-constexpr int kSmRing = 8;            // gram units in LDS: 7 in flight while one is read
+constexpr int kSmRing = 8;            // gram units in LDS: 7 in flight while one is read (gram form)
+constexpr int kSmRingStd = 4;         // standard form: 64 KiB of ring, two blocks per CU
 constexpr int kSmApplyWaves = 8;                     // apply blocks: waves of 128 x 64
 constexpr int kSmApplyThreads = 64 * kSmApplyWaves;
 constexpr int kSmApplyCols = 64 * kSmApplyWaves;     // columns of X per apply tile: one 1 KiB row
@@ -217,15 +218,16 @@ struct SmCopy {
   }
 };
 
-// One unit in slot S: wait for it, refill the slot read last (unit u-1's) with
-// unit u + 7, accumulate the unit's two k-steps. The barrier is a bare
-// s_barrier: __syncthreads' fence would drain every copy in flight.
-template <int S>
+// One unit in slot S of a ring of RING slots: wait for it, refill the slot read
+// last (unit u-1's) with unit u + RING - 1, accumulate the unit's two k-steps.
+// The barrier is a bare s_barrier: __syncthreads' fence would drain every copy
+// in flight.
+template <int RING, int S>
 __device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy, int u, int KT, f32x4 (&acc)[4][2],
                                           int r0, int c0, int lane) {
-  wait_units(min(kSmRing - 2, KT - 1 - u));  // this wave's copies of unit u have landed
+  wait_units(min(RING - 2, KT - 1 - u));  // this wave's copies of unit u have landed
   block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
-  if (u + kSmRing - 1 < KT) copy(ring.s[(S + kSmRing - 1) % kSmRing], u + kSmRing - 1);
+  if (u + RING - 1 < KT) copy(ring.s[(S + RING - 1) % RING], u + RING - 1);
   const char* src = ring.s[S];
   const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -244,23 +246,31 @@ __device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy
 }
 
 // One block of 8 waves per small matrix of the group (grid = matrices).
-__global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCoreArgs args) {
+// RING = kSmRing (gram form: R, Z, Q and RZ take the whole ring afterwards,
+// one block per CU) or kSmRingStd (standard form, steps == 0: R and B fit in
+// four slots, so two blocks share a CU and one's M x M part overlaps the
+// other's gram stream).
+template <int RING>
+__global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_kernel(SmallCoreArgs args) {
 #pragma clang fp contract(off)
+  static_assert(RING == kSmRing || RING == kSmRingStd, "ring depth");
   __shared__ __attribute__((aligned(1024))) char g0[kSmUnit];
   __shared__ __attribute__((aligned(1024))) char g1[kSmUnit];
   __shared__ __attribute__((aligned(1024))) char g2[kSmUnit];
   __shared__ __attribute__((aligned(1024))) char g3[kSmUnit];
-  __shared__ __attribute__((aligned(1024))) char g4[kSmUnit];
-  __shared__ __attribute__((aligned(1024))) char g5[kSmUnit];
-  __shared__ __attribute__((aligned(1024))) char g6[kSmUnit];
-  __shared__ __attribute__((aligned(1024))) char g7[kSmUnit];
   SmRing ring;  // (set member by member: an aggregate initialiser of LDS addresses does not compile)
   ring.s[0] = g0; ring.s[1] = g1; ring.s[2] = g2; ring.s[3] = g3;
-  ring.s[4] = g4; ring.s[5] = g5; ring.s[6] = g6; ring.s[7] = g7;
   // after the gram the ring holds the M x M matrices, two slots each
   SmMat R, Z, Q, RZ;
   R.h[0] = g0; R.h[1] = g1; Z.h[0] = g2; Z.h[1] = g3;
-  Q.h[0] = g4; Q.h[1] = g5; RZ.h[0] = g6; RZ.h[1] = g7;
+  if constexpr (RING == kSmRing) {
+    __shared__ __attribute__((aligned(1024))) char g4[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char g5[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char g6[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char g7[kSmUnit];
+    ring.s[4] = g4; ring.s[5] = g5; ring.s[6] = g6; ring.s[7] = g7;
+    Q.h[0] = g4; Q.h[1] = g5; RZ.h[0] = g6; RZ.h[1] = g7;
+  }
 
   const MatDesc& d = args.descs[blockIdx.x];
   const int wave = wave_id(), lane = lane_id();
@@ -282,31 +292,31 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCor
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  if (0 < KT) copy(ring.s[0], 0);
-  if (1 < KT) copy(ring.s[1], 1);
-  if (2 < KT) copy(ring.s[2], 2);
-  if (3 < KT) copy(ring.s[3], 3);
-  if (4 < KT) copy(ring.s[4], 4);
-  if (5 < KT) copy(ring.s[5], 5);
-  if (6 < KT) copy(ring.s[6], 6);
+#pragma unroll
+  for (int i = 0; i < RING - 1; ++i)
+    if (i < KT) copy(ring.s[i], i);
   int u = 0;
-  for (; u + kSmRing <= KT; u += kSmRing) {
-    gram_unit<0>(ring, copy, u, KT, acc, r0, c0, lane);
-    gram_unit<1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
-    gram_unit<2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
-    gram_unit<3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
-    gram_unit<4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
-    gram_unit<5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
-    gram_unit<6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
-    gram_unit<7>(ring, copy, u + 7, KT, acc, r0, c0, lane);
+  for (; u + RING <= KT; u += RING) {
+    gram_unit<RING, 0>(ring, copy, u, KT, acc, r0, c0, lane);
+    gram_unit<RING, 1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
+    gram_unit<RING, 2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
+    gram_unit<RING, 3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
+    if constexpr (RING == kSmRing) {
+      gram_unit<RING, 4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
+      gram_unit<RING, 5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
+      gram_unit<RING, 6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
+      gram_unit<RING, 7>(ring, copy, u + 7, KT, acc, r0, c0, lane);
+    }
   }
-  if (u < KT) gram_unit<0>(ring, copy, u, KT, acc, r0, c0, lane);
-  if (u + 1 < KT) gram_unit<1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
-  if (u + 2 < KT) gram_unit<2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
-  if (u + 3 < KT) gram_unit<3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
-  if (u + 4 < KT) gram_unit<4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
-  if (u + 5 < KT) gram_unit<5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
-  if (u + 6 < KT) gram_unit<6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
+  if (u < KT) gram_unit<RING, 0>(ring, copy, u, KT, acc, r0, c0, lane);
+  if (u + 1 < KT) gram_unit<RING, 1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
+  if (u + 2 < KT) gram_unit<RING, 2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
+  if constexpr (RING == kSmRing) {
+    if (u + 3 < KT) gram_unit<RING, 3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
+    if (u + 4 < KT) gram_unit<RING, 4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
+    if (u + 5 < KT) gram_unit<RING, 5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
+    if (u + 6 < KT) gram_unit<RING, 6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
+  }
   // R = s²·X Xᵀ (s² = 1/‖X‖² on the unscaled first X): sm_finish's first
   // barrier also ends every wave's reads of the ring, whose first two slots
   // R overwrites (every copy has landed: the last unit waited for all)
@@ -314,10 +324,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_small_core_kernel(SmallCor
 
   // ---- the M x M part of the iteration
   const SmMat* out = &Z;
-  if (args.steps == 0) {
+  if (RING == kSmRingStd || args.steps == 0) {
     const float* k = args.coeffs + 3 * args.it0;
     sm_product(R, R, R, Z, k[2], k[1], wave, lane);  // B = c R R + b R
-  } else {
+  } else if constexpr (RING == kSmRing) {
     for (int i = 0; i < args.steps; ++i) {
       const float* k = args.coeffs + 3 * (args.it0 + i);
       const float a = k[0], b = k[1], c = k[2];
