@@ -562,7 +562,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   const bool small = items[0].plan.small;
   for (int i = 1; i < count; ++i)
     if (items[i].plan.small != small) return fail(PM_EINVAL, "internal: a group mixes small and large matrices");
-  ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov, small ? 2 : ((kWsLayout & kTiledX) ? 1 : 0), 0};
+  ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov, small ? XL_SMALL : ((kWsLayout & kTiledX) ? XL_PANEL : XL_ROW), 0};
   hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
   timing_mark(stream, PM_K_PROLOGUE, group, -1, count, 0.0, b_pro);
   hipLaunchKernelGGL(pm_norm_kernel, dim3(count), dim3(kThreads), 0, stream, ddesc, hp->eps);

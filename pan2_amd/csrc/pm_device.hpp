@@ -63,6 +63,13 @@ struct MatDesc {
   int32_t pad_;
 };
 
+// Layout of the X / Xᵀ buffers a prologue launch writes.
+enum XLayout : int32_t {
+  XL_ROW = 0,    // row-major
+  XL_PANEL = 1,  // the panel layout of ws_off (large matrices)
+  XL_SMALL = 2,  // the panel layout of a small matrix's X (sm_x_off)
+};
+
 struct ProArgs {
   const MatDesc* descs;
   const int32_t* prefix;  // n+1 prefix sums of pro_tiles
@@ -70,7 +77,7 @@ struct ProArgs {
   int32_t mode;
   float mu;
   int32_t nesterov;
-  int32_t layout;         // of X / Xᵀ: 0 row-major, 1 the panel layout (ws_off), 2 small X (sm_x_off)
+  int32_t layout;         // of X / Xᵀ (XLayout)
   int32_t pad_;
 };
 

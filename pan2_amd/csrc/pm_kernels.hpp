@@ -13,7 +13,8 @@ namespace pm {
 //   MODE_STEP: buf <- mu*buf + (1-mu)*g;  u <- (1-mu)*g + mu*buf  (nesterov)
 //              (pan/optim/muon_triton.py:44-48; fp32 math)
 //   MODE_NS:   u <- in
-// X and Xᵀ get bf16(u) (torch casts to bf16 before NS, torch/optim/_muon.py:55)
+// X and Xᵀ get bf16(u) (torch casts to bf16 before NS, torch/optim/_muon.py:55),
+// in the layout ProArgs.layout names
 // and partials[tile] = Σ bf16(u)², the tile's share of ‖X‖² (norm over the
 // bf16 tensor, torch/optim/_muon.py:59).
 // Each thread moves two runs of 8 consecutive elements of a row: 16-byte
@@ -100,7 +101,9 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
   uint16_t* dst_b = d.trans ? d.X[0] : d.XT[0];
   const int64_t ld_b = d.trans ? d.Np : d.Mp;
   const int layout = args.layout;
-  auto x_off = [&](int r, int c, int64_t ld) { return layout == 2 ? sm_x_off(r, c) : ws_off(r, c, ld, layout == 1); };
+  auto x_off = [&](int r, int c, int64_t ld) {
+    return layout == XL_SMALL ? sm_x_off(r, c) : ws_off(r, c, ld, layout == XL_PANEL);
+  };
 
   float ss = 0.0f;
   const int cg = (threadIdx.x & 7) * 8;  // first column of this thread's runs
