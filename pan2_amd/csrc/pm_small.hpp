@@ -136,6 +136,12 @@ __device__ __forceinline__ void sm_finish(const f32x4 (&acc)[4][2], const SmMat&
   __syncthreads();
 }
 
+// Waves 4 and 5 own rows 64..127 of columns 0..63: every element of their
+// tiles lies below the diagonal, which sm_finish neither stores nor mirrors, so
+// they skip the products (fragment reads and MFMAs) and only keep the block's
+// barriers.
+__device__ __forceinline__ bool sm_idle(int r0, int c0) { return r0 > c0 + 31; }
+
 // C = alpha·L·Rᵀ + beta·D on 128 x 128 LDS matrices (K = 128). Every matrix
 // here is symmetric, so L Rᵀ = L R.
 __device__ __forceinline__ void sm_product(const SmMat& L, const SmMat& R, const SmMat& D, const SmMat& C, float alpha,
@@ -147,17 +153,19 @@ __device__ __forceinline__ void sm_product(const SmMat& L, const SmMat& R, const
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if (!sm_idle(r0, c0)) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {  // k = 32s .. 32s+31: logical chunks 4s .. 4s+3
-    bf16x8 a[4], b[2];
+    for (int s = 0; s < 4; ++s) {  // k = 32s .. 32s+31: logical chunks 4s .. 4s+3
+      bf16x8 a[4], b[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)sm_at(L, r0 >> 6, 16 * i + r16, 4 * s + g);
+      for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)sm_at(L, r0 >> 6, 16 * i + r16, 4 * s + g);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = *(const bf16x8*)sm_at(R, c0 >> 6, (c0 & 63) + 16 * j + r16, 4 * s + g);
+      for (int j = 0; j < 2; ++j) b[j] = *(const bf16x8*)sm_at(R, c0 >> 6, (c0 & 63) + 16 * j + r16, 4 * s + g);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
+    }
   }
   sm_finish(acc, D, C, alpha, beta, r0, c0, lane);
 }
@@ -228,6 +236,7 @@ __device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy
   wait_units(min(RING - 2, KT - 1 - u));  // this wave's copies of unit u have landed
   block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
   if (u + RING - 1 < KT) copy(ring.s[(S + RING - 1) % RING], u + RING - 1);
+  if (sm_idle(r0, c0)) return;
   const char* src = ring.s[S];
   const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
