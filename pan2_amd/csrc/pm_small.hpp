@@ -450,20 +450,28 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(sbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
     }
     // X tile: the tile's units are contiguous in HBM (sm_x_off; n0 is a
-    // multiple of 64). Copy q moves rows 8(q%16) .. +7 of unit q/16 (1 KiB);
-    // lane l lands at row 8(q%16) + l/8, stored chunk l%8, so it loads logical
-    // chunk (l%8) ^ swizzle(row). Units past Np read as zeros (buffer bounds).
+    // multiple of 64). Wave w moves unit w, the 64 columns its S X products
+    // read: copy i moves rows 8i .. 8i+7 (1 KiB); lane l lands at row 8i + l/8,
+    // stored chunk l%8, so it loads logical chunk (l%8) ^ swizzle(row). Units
+    // past Np read as zeros (buffer bounds).
+    static_assert(kSmXUnits == kSmApplyWaves, "one unit of the X tile per wave");
     const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(X + sm_x_off(0, n0), (uint32_t)(nx / 64) * kSmUnit);
-    for (int q = w; q < kSmXUnits * (kSm / 8); q += kSmApplyWaves) {
-      const int j = q / (kSm / 8), k = 8 * (q % (kSm / 8)) + (lane >> 3);
+#pragma unroll
+    for (int i = 0; i < kSm / 8; ++i) {
+      const int k = 8 * i + (lane >> 3);
       const int lc = (lane & 7) ^ (((k >> 3) & 3) << 1);  // logical chunk of row k
-      const int voff = 64 * j < nx ? j * kSmUnit + k * 128 + lc * 16 : 0x7fffffff;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + j * kSmUnit + (q % (kSm / 8)) * 1024), 16, voff, 0,
-                                               0, 0);
+      const int voff = 64 * w < nx ? w * kSmUnit + k * 128 + lc * 16 : 0x7fffffff;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + w * kSmUnit + i * 1024), 16, voff, 0, 0, 0);
     }
   }
+  // S is shared: every wave's S copies (issued before its X copies) land
+  // before the block barrier. X is not: a wave waits for its own unit only,
+  // except in the wide FINAL, whose waves read two units each. Bare barriers:
+  // __syncthreads' fence would wait for every copy in flight.
+  wait_vmcnt<kSm / 8>();
+  block_barrier();
   wait_vmcnt<0>();
-  __syncthreads();
+  if (STAGE == ST_FINAL && !d.trans) block_barrier();
   const int r16 = lane & 15, g = lane >> 4;
   // the MFMA fragment of X column n for k-step s (k = 32s + 8g .. +7), read
   // transposed from the tile, element by element
