@@ -1,6 +1,6 @@
 """Parity over seeded random ragged shapes, both Newton–Schulz paths in one call.
 
-36 shapes drawn from a fixed seed: short sides from 1 to 700 (so both the
+Standard form: 36 shapes drawn from a fixed seed: short sides from 1 to 700 (so both the
 small-matrix kernels, short side <= 128, and the grouped GEMM engine with its
 padded panels run), long sides up to 3000, wide and tall, none a multiple of
 256 by construction of the draw (the padding and the panel layouts' partial
@@ -10,7 +10,12 @@ checked against a float32 restatement of the standard quintic on the GPU
 (TORCH/optim/_muon.py:55-69), and a second call with every matrix on its own
 must give the same bits (grouping changes no arithmetic).
 
-Gate: relative Frobenius error <= max(2e-2, 1.25 x the error of torch's own
+The gram form (PAN 2's production form) gets its own sweep of 20 smaller
+shapes, gated as in the gram-form tests: against the fp64 standard NS within
+max(2e-2, 1.25 x the error of the oracle's bf16 gram form on the same input),
+and within sqrt(2) x that of the oracle itself.
+
+Gate (standard form): relative Frobenius error <= max(2e-2, 1.25 x the error of torch's own
 bf16 NS, the reference's CPU path, on the same input). Very narrow shapes
 (short side a few dozen, long side thousands) take any bf16 NS past 2e-2:
 torch's stock bf16 quintic measures 0.021-0.028 against fp32 at 42 x 2504 and
@@ -21,6 +26,7 @@ import pytest
 import torch
 from torch.optim._muon import _zeropower_via_newtonschulz as torch_ns
 
+from oracle import muon_ref
 from pan2_amd import _lib
 
 pytestmark = pytest.mark.gpu
@@ -29,12 +35,12 @@ DEV = "cuda:0"
 COEFFS = (3.4445, -4.7750, 2.0315)
 
 
-def shapes(n=36, seed=20251201):
+def shapes(n=36, seed=20251201, max_short=700, max_long=3000):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
-        short = int(rng.integers(1, 129)) if i % 2 == 0 else int(rng.integers(129, 701))
-        long = int(rng.integers(short, 3001))
+        short = int(rng.integers(1, 129)) if i % 2 == 0 else int(rng.integers(129, max_short + 1))
+        long = int(rng.integers(short, max_long + 1))
         if long % 256 == 0:
             long += 1
         if short % 256 == 0:
@@ -74,5 +80,28 @@ def test_random_ragged_shapes_one_call():
     singles = [torch.empty_like(o) for o in outs]
     for x, o in zip(xs, singles):
         _lib.newton_schulz_into([(x, o)], ns_coefficients=COEFFS)
+    for s, o, o1 in zip(shp, outs, singles):
+        assert torch.equal(o, o1), s
+
+
+def test_random_ragged_shapes_gram_form():
+    shp = shapes(n=20, seed=777, max_short=300, max_long=1500)
+    print(f"random shapes (gram form): {shp}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    xs = [torch.randn(s, generator=gen, device=DEV, dtype=torch.float32) for s in shp]
+    outs = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shp]
+    _lib.newton_schulz_into(list(zip(xs, outs)), ns_coefficients=COEFFS, ns_form="gram", workspace_limit=16 << 20)
+    for s, x, o in zip(shp, xs, outs):
+        g = x.cpu().numpy()
+        ref = muon_ref.ns_standard(g, precision="fp64")
+        oracle = muon_ref.ns_gram(g, precision="bf16")
+        gate = max(2e-2, 1.25 * float(np.linalg.norm(oracle - ref) / np.linalg.norm(ref)))
+        got = o.double().cpu().numpy()
+        err = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+        assert err <= gate, (s, err, gate)
+        assert float(np.linalg.norm(got - oracle) / np.linalg.norm(oracle)) <= np.sqrt(2) * gate, s
+    singles = [torch.empty_like(o) for o in outs]
+    for x, o in zip(xs, singles):
+        _lib.newton_schulz_into([(x, o)], ns_coefficients=COEFFS, ns_form="gram")
     for s, o, o1 in zip(shp, outs, singles):
         assert torch.equal(o, o1), s
