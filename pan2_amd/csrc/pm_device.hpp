@@ -109,25 +109,6 @@ constexpr int kWsLayout = kTiledX | kTiledS;
 
 // ---------------------------------------------------------------- helpers
 
-// Element offset of (r, c) in a workspace matrix with ld columns.
-// Row-major: r·ld + c. Panel layout (tiled): the matrix is cut into panels of
-// kTile rows and each panel into units of 64 columns; unit (r/256, c/64) is a
-// contiguous 32 KiB block of 256 rows of 128 bytes. A panel starts where it
-// does row-major (row 256·i), and one unit of a panel is exactly what the GEMM
-// engine streams into LDS per K step, so each of its 1 KiB copies (8 rows) reads
-// contiguous memory. Needs ld a multiple of 64 and rows a multiple of 256 (the
-// engine's padded extents). Runs of up to 8 elements starting at a multiple of
-// their length stay contiguous in both layouts.
-__device__ __forceinline__ int64_t ws_off(int r, int c, int64_t ld, bool tiled) {
-  if (!tiled) return (int64_t)r * ld + c;
-  return ((((int64_t)(r >> 8) * (ld >> 6)) + (c >> 6)) << 14) + ((r & 255) << 6) + (c & 63);
-}
-
-// The same layout for a small matrix's X (128 x Np, one panel of 128 rows):
-// unit c/64 is a contiguous 16 KiB block of 128 rows of 128 bytes.
-__device__ __forceinline__ int64_t sm_x_off(int r, int c) {
-  return ((int64_t)(c >> 6) << 13) + (r << 6) + (c & 63);
-}
 
 __device__ __forceinline__ uint16_t f2bf(float f) {
   __bf16 h = (__bf16)f;  // v_cvt_pk_bf16_f32: round to nearest even, NaN kept

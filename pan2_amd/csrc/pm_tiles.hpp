@@ -1,6 +1,9 @@
-// Work-item -> tile decoders of the GEMM stages. Plain arithmetic, compiled
-// for the device by hipcc and for the host by the CPU tests (g++).
+// Work-item -> tile decoders of the GEMM stages and the workspace layouts.
+// Plain arithmetic, compiled for the device by hipcc and for the host by the
+// CPU tests (g++).
 #pragma once
+
+#include <stdint.h>
 
 #if defined(__HIPCC__)
 #define PM_HD __host__ __device__ __forceinline__
@@ -65,5 +68,24 @@ PM_HD void sym_tile(int lt, int nt, int& ti, int& tj) {
     tj = g0 + gm + rem / gm;
   }
 }
+
+// Element offset of (r, c) in a workspace matrix with ld columns.
+// Row-major: r·ld + c. Panel layout (tiled): the matrix is cut into panels of
+// 256 rows (the GEMM tile) and each panel into units of 64 columns; unit
+// (r/256, c/64) is a contiguous 32 KiB block of 256 rows of 128 bytes. A panel
+// starts where it does row-major (row 256·i), and one unit of a panel is
+// exactly what the GEMM engine streams into LDS per K step, so each of its
+// 1 KiB copies (8 rows) reads contiguous memory. Needs ld a multiple of 64 and
+// rows a multiple of 256 (the engine's padded extents). Runs of up to 8
+// elements starting at a multiple of their length stay contiguous in both
+// layouts.
+PM_HD int64_t ws_off(int r, int c, int64_t ld, bool tiled) {
+  if (!tiled) return (int64_t)r * ld + c;
+  return ((((int64_t)(r >> 8) * (ld >> 6)) + (c >> 6)) << 14) + ((r & 255) << 6) + (c & 63);
+}
+
+// The same layout for a small matrix's X (128 x Np, one panel of 128 rows):
+// unit c/64 is a contiguous 16 KiB block of 128 rows of 128 bytes.
+PM_HD int64_t sm_x_off(int r, int c) { return ((int64_t)(c >> 6) << 13) + (r << 6) + (c & 63); }
 
 }  // namespace pm
