@@ -370,7 +370,7 @@ def main() -> int:
     ap.add_argument("--ns-form", default="standard", choices=("standard", "gram"),
                     help="standard: torch's quintic (the BASELINE metric); gram: PAN 2's production gram form, "
                          "reported with its own (smaller) executed FLOP count")
-    ap.add_argument("--cpu-budget", type=float, default=25.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=45.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workspace-gib", type=float, default=0.0, help="libpanmuon workspace cap (0 = default)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -521,9 +521,9 @@ def main() -> int:
             "kind": "reference",
             "sample": ("stock torch.optim.Muon step (the reference's float-lr path, pan/optim/muon.py:126-154), "
                        f"fp32, one matrix per distinct shape ({', '.join(cb['timed_shapes'])}) timed on "
-                       f"{cb['cores']} host threads (short steps: median of 3 or 5 after a warm-up; "
-                       f"repeats {cb['repeats']}); " + ("extrapolated to the config's counts by shape"
-                                                        if cb["extrapolated"] else "full config")),
+                       f"{cb['cores']} host threads (one warm-up step, then the median of {cb['repeats']} "
+                       "steps per shape); " + ("extrapolated to the config's counts by shape"
+                                               if cb["extrapolated"] else "full config")),
             "cpu": cb["cpu"],
         }
 

@@ -43,10 +43,14 @@ extern "C" {
 
 #define PM_ABI_VERSION 2
 
-/* Element types accepted for params, grads, momentum buffers and updates. */
+/* Element types accepted for params, grads, momentum buffers and updates.
+ * PM_DTYPE_F16 is accepted by pm_adam_step only, as torch's fused Adam takes
+ * fp16 params and state (torch/optim/adam.py:803-898); the Muon entry points
+ * take f32 and bf16. */
 enum pm_dtype {
   PM_DTYPE_F32 = 0,
-  PM_DTYPE_BF16 = 1
+  PM_DTYPE_BF16 = 1,
+  PM_DTYPE_F16 = 2
 };
 
 /* pm_hparams.ns_form */

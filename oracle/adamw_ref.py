@@ -23,8 +23,15 @@ f32 = np.float32
 
 
 def _store(x, dtype: str):
+    """The stored value of an fp32 result: "f32" as is, "bf16" or "f16" rounded
+    to nearest even (numpy's IEEE half cast for f16)."""
     x = np.asarray(x, dtype=f32)
-    return round_bf16(x) if dtype == "bf16" else x
+    if dtype == "bf16":
+        return round_bf16(x)
+    if dtype == "f16":
+        with np.errstate(over="ignore"):  # beyond fp16's range: inf, as torch's cast gives
+            return x.astype(np.float16).astype(f32)
+    return x
 
 
 def lerp(start, end, w):
@@ -41,7 +48,7 @@ def adam_step(param, grad, exp_avg, exp_avg_sq, step, *, lr: float, beta1: float
     """One step; returns (param, exp_avg, exp_avg_sq, max_exp_avg_sq, step).
 
     Arrays hold the values of the stored tensors as float32; dtypes gives the
-    storage of (param, exp_avg, exp_avg_sq) ("f32" or "bf16"). lr, betas, eps
+    storage of (param, exp_avg, exp_avg_sq) ("f32", "bf16" or "f16"). lr, betas, eps
     and weight_decay are Python floats. step is the stored step before this
     call (torch increments it first, TORCH/optim/adam.py:414).
     """

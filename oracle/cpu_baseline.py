@@ -38,10 +38,12 @@ def cpu_info() -> dict:
     return {"model": model, "avx512_bf16": "avx512_bf16" in flags, "amx_bf16": "amx_bf16" in flags}
 
 
-def time_stock_muon_step(shape, *, threads: int, seed: int = 0, repeats: int = 1, warmup: bool = False,
+def time_stock_muon_step(shape, *, threads: int, seed: int = 0, repeats=1, warmup: bool = False,
                          adjust_lr_fn="match_rms_adamw", stock_fns=None) -> float:
     """Seconds for one stock torch.optim.Muon step on one fp32 matrix (median).
 
+    repeats: a count, or a function of the warm-up step's seconds giving the
+    count (then the warm-up runs whatever `warmup` says).
     stock_fns: (zeropower, single_tensor_muon) to install while timing, for
     processes where patch_muon already replaced torch's module globals.
     """
@@ -56,8 +58,11 @@ def time_stock_muon_step(shape, *, threads: int, seed: int = 0, repeats: int = 1
     if stock_fns is not None:
         tm._zeropower_via_newtonschulz, tm._single_tensor_muon = stock_fns
     try:
-        if warmup:
+        if warmup or callable(repeats):
+            t0 = time.perf_counter()
             opt.step()
+            if callable(repeats):
+                repeats = repeats(time.perf_counter() - t0)
         times = []
         for _ in range(repeats):
             t0 = time.perf_counter()
@@ -68,8 +73,13 @@ def time_stock_muon_step(shape, *, threads: int, seed: int = 0, repeats: int = 1
     return statistics.median(times)
 
 
-def baseline(shapes, *, threads: int | None = None, budget_s: float = 30.0, stock_fns=None) -> dict:
+def baseline(shapes, *, threads: int | None = None, budget_s: float = 45.0, stock_fns=None) -> dict:
     """Time one matrix per distinct shape and extrapolate to the full list.
+
+    Every shape timed gets one warm-up step, then the median of 3 steps (5 for
+    a step under 2% of the budget). Shapes are taken smallest first; once the
+    budget is spent, the shapes not yet timed are scaled from the largest timed
+    one by dense NS work (and the result is labelled extrapolated).
 
     Returns {"step_ms": extrapolated ms for all shapes, "cores": threads,
     "sample": description, "per_shape_ms": {...}}.
@@ -81,18 +91,16 @@ def baseline(shapes, *, threads: int | None = None, budget_s: float = 30.0, stoc
     spent = 0.0
     repeats_used = {}
     for shape in sorted(counts, key=lambda s: s[0] * s[1]):
-        t = time_stock_muon_step(shape, threads=threads, stock_fns=stock_fns)
-        spent += t
-        # a step that is short against the budget is re-timed after this warm-up:
-        # the median of 5 (under 2% of the budget) or of 3 (under 5%)
-        reps = 5 if t < 0.02 * budget_s else 3 if t < 0.05 * budget_s else 1
-        if reps > 1:
-            t = time_stock_muon_step(shape, threads=threads, stock_fns=stock_fns, repeats=reps)
-            spent += reps * t
-        per_shape[shape] = t
-        repeats_used[shape] = reps
         if spent > budget_s:
             break
+        t0 = time.perf_counter()
+
+        def reps(first, shape=shape):  # from the warm-up step's time
+            repeats_used[shape] = 5 if first < 0.02 * budget_s else 3
+            return repeats_used[shape]
+
+        per_shape[shape] = time_stock_muon_step(shape, threads=threads, stock_fns=stock_fns, repeats=reps)
+        spent += time.perf_counter() - t0
     missing = [s for s in counts if s not in per_shape]
     if missing:
         # scale the largest timed shape by dense NS work for shapes not timed

@@ -18,6 +18,7 @@ ABI_VERSION = 2
 
 PM_DTYPE_F32 = 0
 PM_DTYPE_BF16 = 1
+PM_DTYPE_F16 = 2  # pm_adam_step only
 
 # Newton–Schulz organisation (pm_hparams.ns_form)
 PM_NS_STANDARD = 0
@@ -478,12 +479,22 @@ _PM_ADAM_NP = np.dtype({
 })
 
 
+ADAM_DTYPES = {torch.float32: PM_DTYPE_F32, torch.bfloat16: PM_DTYPE_BF16, torch.float16: PM_DTYPE_F16}
+
+
+def adam_dtype_code(t: torch.Tensor) -> int:
+    """pm_adam_step's dtype code of a tensor: float32, bfloat16 or float16."""
+    code = ADAM_DTYPES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"pm_adam_step supports float32, bfloat16 and float16 tensors, got {t.dtype}")
+    return code
+
+
 def _dtype_codes(ts) -> int | list[int]:
     kinds = {t.dtype for t in ts}
     if len(kinds) == 1:
-        t = ts[0]
-        return dtype_code(t)
-    return [dtype_code(t) for t in ts]
+        return adam_dtype_code(ts[0])
+    return [adam_dtype_code(t) for t in ts]
 
 
 def _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev):

@@ -170,20 +170,24 @@ struct Item {
 
 // Descriptor uploads go through pinned staging buffers: the host table is
 // copied into one, and an asynchronous copy on the caller's stream moves it
-// to the workspace, so the host never waits for the stream. A buffer is
-// reused once the event recorded after its copy has completed; the pool
-// grows while every buffer is still in flight (a call queued far behind the
-// GPU), up to kMaxStaging buffers per device, after which the oldest is
-// waited for.
+// to the workspace, so the host does not wait for the stream. A buffer is
+// reused once the event recorded after its copy has completed (the smallest
+// free one that holds the table, else the largest free one, regrown). The
+// pool grows while every buffer is still in flight (calls queued far behind
+// the GPU), up to kMaxStaging buffers per device; only a call made while
+// kMaxStaging uploads of its device are still queued waits, for the oldest
+// of them (the lowest sequence number).
 struct Staging {
   int device;
   void* host;
   size_t bytes;
   hipEvent_t done;
+  uint64_t seq;  // order in which the buffer's current copy was enqueued
 };
-constexpr size_t kMaxStaging = 64;
+constexpr size_t kMaxStaging = 1024;
 std::mutex g_stage_mu;
 std::vector<Staging> g_stage;
+uint64_t g_stage_seq = 0;
 
 int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
   int dev = 0;
@@ -196,9 +200,10 @@ int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
     Staging& c = g_stage[i];
     if (c.device != dev) continue;
     ++mine;
-    if (oldest == SIZE_MAX) oldest = i;
+    if (oldest == SIZE_MAX || c.seq < g_stage[oldest].seq) oldest = i;
     if (hipEventQuery(c.done) != hipSuccess) continue;  // its copy is still queued
-    if (!s || c.bytes > s->bytes) s = &c;              // a free buffer, the largest
+    const bool fits = c.bytes >= bytes, s_fits = s && s->bytes >= bytes;
+    if (!s || (fits && (!s_fits || c.bytes < s->bytes)) || (!fits && !s_fits && c.bytes > s->bytes)) s = &c;
   }
   if (!s && mine >= kMaxStaging) {
     s = &g_stage[oldest];
@@ -206,12 +211,13 @@ int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
     if (e != hipSuccess) return hip_fail(e, "staging event");
   }
   if (!s) {
-    Staging c{dev, nullptr, 0, nullptr};
+    Staging c{dev, nullptr, 0, nullptr, 0};
     e = hipEventCreateWithFlags(&c.done, hipEventDisableTiming);
     if (e != hipSuccess) return hip_fail(e, "staging event create");
     g_stage.push_back(c);
     s = &g_stage.back();
   }
+  s->seq = ++g_stage_seq;
   if (s->bytes < bytes) {
     if (s->host) {
       e = hipHostFree(s->host);  // its copy has completed
@@ -240,14 +246,20 @@ struct TimingRec {
   pm_launch_time info;
   hipEvent_t begin, end;
 };
+// Shared by every thread of the process: `on` is atomic and the rest is
+// guarded by `mu`. A record spans from the previous event of the same stream,
+// so records of calls that interleave on several streams at once are dropped
+// rather than mismeasured; timing is meant for one stream at a time.
 struct Timing {
-  bool on = false;
+  std::atomic<bool> on{false};
+  std::mutex mu;
   std::vector<hipEvent_t> pool;
   std::vector<TimingRec> recs;
   hipEvent_t last = nullptr;
   hipStream_t last_stream = nullptr;
 } g_timing;
 
+// Caller holds g_timing.mu.
 hipEvent_t timing_event() {
   if (!g_timing.pool.empty()) {
     hipEvent_t e = g_timing.pool.back();
@@ -261,7 +273,8 @@ hipEvent_t timing_event() {
 
 // Marks the start of a timed sequence on `stream`.
 void timing_begin(hipStream_t stream) {
-  if (!g_timing.on) return;
+  if (!g_timing.on.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lock(g_timing.mu);
   hipEvent_t e = timing_event();
   if (!e) return;
   if (hipEventRecord(e, stream) != hipSuccess) {
@@ -274,7 +287,9 @@ void timing_begin(hipStream_t stream) {
 
 // Records the end of the launch just enqueued on `stream`.
 void timing_mark(hipStream_t stream, int kind, int group, int iteration, int nmat, double flops, double bytes) {
-  if (!g_timing.on || !g_timing.last || g_timing.last_stream != stream) return;
+  if (!g_timing.on.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  if (!g_timing.last || g_timing.last_stream != stream) return;
   hipEvent_t e = timing_event();
   if (!e) return;
   if (hipEventRecord(e, stream) != hipSuccess) {
@@ -482,8 +497,23 @@ int run_small(Launcher& L, const pm_hparams* hp) {
 
 // Runs one group: items[0, count) share the workspace `ws` and are all small
 // or all not.
+// How a group's descriptor table reaches the workspace: an asynchronous copy
+// from a pinned staging buffer (upload).
+enum class TablePath { kStaged };
+
 int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
-              double lr_host, char* ws, hipStream_t stream) {
+              double lr_host, char* ws, hipStream_t stream, TablePath path) {
+  // plan_groups keeps small and engine matrices in separate groups: the engine's
+  // workspace matrices are in the panel layout, small matrices' X row-major
+  const bool small = items[0].plan.small;
+  for (int i = 1; i < count; ++i)
+    if (items[i].plan.small != small) return fail(PM_EINVAL, "internal: a group mixes small and large matrices");
+  // The FINAL epilogue is compiled per param dtype; plan_groups keeps a group's
+  // params of one dtype (MODE_NS writes bf16).
+  for (int i = 1; i < count; ++i)
+    if (mode == MODE_STEP && items[i].desc.p_dt != items[0].desc.p_dt)
+      return fail(PM_EINVAL, "internal: a group mixes param dtypes");
+
   const int form = hp->ns_form;
   // Table first, then per-matrix buffers.
   const size_t tb = table_bytes(count, gemm_launches(hp));
@@ -533,6 +563,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     full[i + 1] = full[i] + full_tiles(p);
     max_mp = std::max(max_mp, p.Mp);
   }
+  (void)path;
   int rc = upload(host.data(), tb, ws, stream);
   if (rc) return rc;
   timing_begin(stream);
@@ -557,11 +588,6 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   const int32_t* dfull = (const int32_t*)(ws + ((char*)full - host.data()));
   int32_t* dqueues = (int32_t*)(ws + ((const char*)queues - host.data()));
 
-  // run_all keeps small and engine matrices in separate groups: the engine's
-  // workspace matrices are in the panel layout, small matrices' X row-major
-  const bool small = items[0].plan.small;
-  for (int i = 1; i < count; ++i)
-    if (items[i].plan.small != small) return fail(PM_EINVAL, "internal: a group mixes small and large matrices");
   ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov, small ? XL_SMALL : ((kWsLayout & kTiledX) ? XL_PANEL : XL_ROW), 0};
   hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
   timing_mark(stream, PM_K_PROLOGUE, group, -1, count, 0.0, b_pro);
@@ -569,12 +595,6 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   timing_mark(stream, PM_K_NORM, group, -1, count, 0.0, 0.0);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prologue launch");
-
-  // The FINAL epilogue is compiled per param dtype; run_all keeps a group's
-  // params of one dtype (MODE_NS writes bf16).
-  for (int i = 1; i < count; ++i)
-    if (mode == MODE_STEP && items[i].desc.p_dt != items[0].desc.p_dt)
-      return fail(PM_EINVAL, "internal: a group mixes param dtypes");
 
   Launcher L{};
   L.ga.descs = ddesc;
@@ -603,22 +623,19 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   return form == NS_GRAM ? run_gram(L, hp, max_mp) : run_standard(L, hp);
 }
 
-// Sorts items by descending work (longest tiles first), packs them into
-// groups that fit the workspace and runs each group in turn.
-int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const float* lr_dev, double lr_host,
-            void* workspace, size_t ws_bytes, hipStream_t stream) {
-  if (items.empty()) return PM_OK;
-  if (!workspace) return fail(PM_EINVAL, "workspace is NULL");
-  if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
-  // params of one dtype together (one FINAL epilogue per launch), small
-  // matrices apart from the rest (other kernels), then longest tiles first
+// Sorts items (params of one dtype together, small matrices apart, then
+// longest tiles first) and packs them into groups [begin, end) whose
+// workspace fits ws_bytes. Fails, before anything is enqueued, when a matrix
+// does not fit on its own.
+int plan_groups(std::vector<Item>& items, const pm_hparams* hp, size_t ws_bytes,
+                std::vector<std::pair<size_t, size_t>>& groups) {
   std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) {
     if (x.desc.p_dt != y.desc.p_dt) return x.desc.p_dt < y.desc.p_dt;
     if (x.plan.small != y.plan.small) return y.plan.small;
     return x.plan.Np != y.plan.Np ? x.plan.Np > y.plan.Np : x.plan.Mp > y.plan.Mp;
   });
+  groups.clear();
   size_t i = 0;
-  int group = 0;
   while (i < items.size()) {
     size_t j = i, need = 0;
     while (j < items.size()) {
@@ -632,10 +649,27 @@ int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const floa
     if (j == i)
       return fail(PM_EWORKSPACE, "workspace of %zu bytes cannot hold a %dx%d matrix (needs %zu)", ws_bytes,
                   items[i].plan.rows, items[i].plan.cols, table_bytes(1, gemm_launches(hp)) + items[i].plan.ws);
-    const int rc = run_group(items.data() + i, (int)(j - i), group++, hp, mode, lr_dev, lr_host,
-                             (char*)workspace, stream);
-    if (rc) return rc;
+    groups.emplace_back(i, j);
     i = j;
+  }
+  return PM_OK;
+}
+
+// Plans every group first (so a workspace too small for some matrix fails
+// before any momentum or param is touched), then runs the groups in turn on
+// the one workspace.
+int run_all(std::vector<Item>& items, const pm_hparams* hp, int mode, const float* lr_dev, double lr_host,
+            void* workspace, size_t ws_bytes, hipStream_t stream, TablePath path = TablePath::kStaged) {
+  if (items.empty()) return PM_OK;
+  if (!workspace) return fail(PM_EINVAL, "workspace is NULL");
+  if ((uintptr_t)workspace % kAlign) return fail(PM_EINVAL, "workspace must be %zu-byte aligned", kAlign);
+  std::vector<std::pair<size_t, size_t>> groups;
+  if (int rc = plan_groups(items, hp, ws_bytes, groups)) return rc;
+  for (size_t g = 0; g < groups.size(); ++g) {
+    const auto [i, j] = groups[g];
+    const int rc = run_group(items.data() + i, (int)(j - i), (int)g, hp, mode, lr_dev, lr_host, (char*)workspace,
+                             stream, path);
+    if (rc) return rc;
   }
   return PM_OK;
 }
@@ -784,13 +818,14 @@ int pm_step_param(void* param, int32_t param_dtype, const void* update, int32_t 
 }
 
 int pm_timing_enable(int on) {
-  g_timing.on = on != 0;
+  g_timing.on.store(on != 0, std::memory_order_relaxed);
   return PM_OK;
 }
 
 int pm_timing_read(pm_launch_time* out, int max) {
   g_err.clear();
   if (max < 0 || (max > 0 && !out)) return fail(PM_EINVAL, "bad output buffer");
+  std::lock_guard<std::mutex> lock(g_timing.mu);
   int n = 0;
   for (TimingRec& r : g_timing.recs) {
     hipError_t e = hipEventSynchronize(r.end);
@@ -938,9 +973,10 @@ int pm_adam_step(const pm_adam_tensor* ts, int n, const pm_adam_hparams* hp, con
     if (t.numel > 0 && (!t.param || !t.grad || !t.exp_avg || !t.exp_avg_sq))
       return fail(PM_EINVAL, "tensor %d: NULL tensor pointer", i);
     if (hp->amsgrad && t.numel > 0 && !t.max_exp_avg_sq) return fail(PM_EINVAL, "tensor %d: amsgrad needs max_exp_avg_sq", i);
-    if (!valid_dtype(t.param_dtype) || !valid_dtype(t.grad_dtype) || !valid_dtype(t.exp_avg_dtype) ||
-        !valid_dtype(t.exp_avg_sq_dtype))
-      return fail(PM_EDTYPE, "tensor %d: dtypes must be f32 or bf16", i);
+    auto adam_dtype = [](int32_t dt) { return valid_dtype(dt) || dt == PM_DTYPE_F16; };
+    if (!adam_dtype(t.param_dtype) || !adam_dtype(t.grad_dtype) || !adam_dtype(t.exp_avg_dtype) ||
+        !adam_dtype(t.exp_avg_sq_dtype))
+      return fail(PM_EDTYPE, "tensor %d: dtypes must be f32, bf16 or f16", i);
     const int64_t chunks = (t.numel + kAdamChunk - 1) / kAdamChunk;
     if (prefix[i] + chunks > INT32_MAX) return fail(PM_EINVAL, "too many elements in one call");
     prefix[i + 1] = (int32_t)(prefix[i] + chunks);

@@ -41,6 +41,52 @@ struct AdamArgs {
   const float* found_inf;   // skip the update when *found_inf != 0, or null
 };
 
+// Eight consecutive elements of an f32, bf16 or f16 tensor as fp32 (f32 and
+// bf16 through the prologue's load8 / store8; f16 here, 16-byte vectors when
+// aligned). f16 results are rounded to nearest even, as torch's fused kernel
+// stores its fp32 results.
+__device__ __forceinline__ void adam_load8(const void* base, int32_t dt, int64_t off, bool vec, int valid,
+                                           float (&v)[8]) {
+  if (dt != DT_F16) {
+    load8(base, dt, off, vec, true, valid, v);
+    return;
+  }
+  const _Float16* h = (const _Float16*)base + off;
+  if (vec && valid >= 8) {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    const f16x8 a = *(const f16x8*)h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = e < valid ? (float)h[e] : 0.0f;
+}
+
+__device__ __forceinline__ void adam_store8(void* base, int32_t dt, int64_t off, bool vec, int valid,
+                                            const float (&v)[8]) {
+  if (dt != DT_F16) {
+    store8(base, dt, off, vec, valid, v);
+    return;
+  }
+  _Float16* h = (_Float16*)base + off;
+  if (vec && valid >= 8) {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    f16x8 a;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = (_Float16)v[e];
+    *(f16x8*)h = a;
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (e < valid) h[e] = (_Float16)v[e];
+}
+
+__device__ __forceinline__ bool adam_vec_ok(const void* base, int32_t dt) {
+  return (uintptr_t)base % 16 == 0 && (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
+}
+
 // step += 1 for every tensor (TORCH/optim/adam.py:877), less found_inf, which
 // torch subtracts again after a skipped update (:895-898).
 __global__ __launch_bounds__(kThreads) void pm_adam_count_kernel(const AdamDesc* descs, int n,
@@ -78,24 +124,24 @@ __global__ __launch_bounds__(kThreads) void pm_adam_kernel(AdamArgs a) {
   // decoupled decay: param.mul_(1 - lr * weight_decay) (:419)
   const float wdf = a.lr_dev ? 1.0f - (float)lr * a.wd : (float)(1.0 - lr * a.wdd);
   const float scale = a.grad_scale ? *a.grad_scale : 1.0f;
-  const bool pv = vec_ok(d.p, d.p_dt, 8), gv = vec_ok(d.g, d.g_dt, 8), mv = vec_ok(d.m, d.m_dt, 8),
-             vv = vec_ok(d.v, d.v_dt, 8), xv = a.amsgrad && vec_ok(d.vmax, d.v_dt, 8);
+  const bool pv = adam_vec_ok(d.p, d.p_dt), gv = adam_vec_ok(d.g, d.g_dt), mv = adam_vec_ok(d.m, d.m_dt),
+             vv = adam_vec_ok(d.v, d.v_dt), xv = a.amsgrad && adam_vec_ok(d.vmax, d.v_dt);
 #pragma unroll 1
   for (int it = 0; it < kAdamChunk / (kThreads * 8); ++it) {
     const int64_t off = base + ((int64_t)it * kThreads + threadIdx.x) * 8;
     if (off >= d.n) break;
     const int valid = d.n - off >= 8 ? 8 : (int)(d.n - off);
     float p[8], g[8], m[8], v[8], x[8];
-    load8(d.p, d.p_dt, off, pv, true, valid, p);
-    load8(d.g, d.g_dt, off, gv, true, valid, g);
-    load8(d.m, d.m_dt, off, mv, true, valid, m);
-    load8(d.v, d.v_dt, off, vv, true, valid, v);
-    if (a.amsgrad) load8(d.vmax, d.v_dt, off, xv, true, valid, x);
+    adam_load8(d.p, d.p_dt, off, pv, valid, p);
+    adam_load8(d.g, d.g_dt, off, gv, valid, g);
+    adam_load8(d.m, d.m_dt, off, mv, valid, m);
+    adam_load8(d.v, d.v_dt, off, vv, valid, v);
+    if (a.amsgrad) adam_load8(d.vmax, d.v_dt, off, xv, valid, x);
     if (a.grad_scale) {
       // the fused kernel leaves the grads unscaled (a GradScaler's unscale_)
 #pragma unroll
       for (int e = 0; e < 8; ++e) g[e] = g[e] / scale;
-      store8(d.g, d.g_dt, off, gv, valid, g);
+      adam_store8(d.g, d.g_dt, off, gv, valid, g);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -116,10 +162,10 @@ __global__ __launch_bounds__(kThreads) void pm_adam_kernel(AdamArgs a) {
       const float denom = sqrtf(vh) / bc2_sqrt + a.eps;  // (:541-545)
       p[e] = pe + neg_step * (m[e] / denom);             // param.addcdiv_(exp_avg, denom, value=-step_size) (:547)
     }
-    store8(d.p, d.p_dt, off, pv, valid, p);
-    store8(d.m, d.m_dt, off, mv, valid, m);
-    store8(d.v, d.v_dt, off, vv, valid, v);
-    if (a.amsgrad) store8(d.vmax, d.v_dt, off, xv, valid, x);
+    adam_store8(d.p, d.p_dt, off, pv, valid, p);
+    adam_store8(d.m, d.m_dt, off, mv, valid, m);
+    adam_store8(d.v, d.v_dt, off, vv, valid, v);
+    if (a.amsgrad) adam_store8(d.vmax, d.v_dt, off, xv, valid, x);
   }
 }
 

@@ -25,7 +25,9 @@ constexpr int kThreads = 256;    // elementwise/prologue blocks: 4 waves of 64 l
 constexpr int kGemmThreads = 512;  // GEMM blocks: 8 waves, two per SIMD
 constexpr int kProTile = 64;     // prologue tile edge
 
-enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
+// DT_F16 is accepted by the Adam step only (torch's fused Adam takes fp16
+// params and state); the Muon path takes f32 and bf16.
+enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 // GRAM: S[sc] = X Xᵀ. SYMM: S[sc] = alpha·S[sl]·S[sr]ᵀ + beta·S[sd] (symmetric
 // result). UPDATE / FINAL: X' = a·X + S[sl]·X (FINAL fused with the param step).
 enum Stage : int32_t { ST_GRAM = 0, ST_SYMM = 1, ST_UPDATE = 2, ST_FINAL = 3 };

@@ -11,6 +11,11 @@ step counts and the element update run as two HIP launches on the current
 stream, with no host synchronisation. The optimizer object, its param groups
 and its state (``step``, ``exp_avg``, ``exp_avg_sq``) stay torch's, so
 state_dict and checkpoints are unchanged.
+
+Tensors the library does not take (float64, complex, or on the CPU) go to
+torch's own fused Adam, saved when this module is imported, exactly as an
+unpatched process would run them; fp32, bf16 and fp16 device tensors go to
+``pm_adam_step``.
 """
 from __future__ import annotations
 
@@ -23,11 +28,19 @@ from .. import _lib
 
 # torch.optim does not keep its adam submodule as an attribute
 _adam_module = importlib.import_module("torch.optim.adam")
+# torch's own fused Adam, for the tensors pm_adam_step does not take
+_torch_fused_adam = _adam_module._fused_adam
 
 
 def _scalar(x):
     """A 1-element tensor beta becomes a Python float (torch's _to_scalar)."""
     return x.item() if isinstance(x, Tensor) else x
+
+
+def _native(i, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, amsgrad) -> bool:
+    """Does pm_adam_step take tensor i: real fp32 / bf16 / fp16 device tensors throughout?"""
+    ts = [params[i], grads[i], exp_avgs[i], exp_avg_sqs[i]] + ([max_exp_avg_sqs[i]] if amsgrad else [])
+    return all(t.is_cuda and t.dtype in _lib.ADAM_DTYPES for t in ts)
 
 
 @torch.compiler.disable
@@ -58,13 +71,24 @@ def _fused_adam(
         return
     if differentiable:
         raise RuntimeError("Adam with fused=True does not support differentiable=True")
-    if has_complex:
-        raise NotImplementedError("pan2_amd Adam has no complex-parameter path")
+    mine = [_native(i, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, amsgrad) for i in range(len(params))]
+    if not all(mine):
+        rest = [i for i, m in enumerate(mine) if not m]
+        pick = lambda xs: [xs[i] for i in rest] if xs else xs  # noqa: E731
+        _torch_fused_adam(
+            pick(params), pick(grads), pick(exp_avgs), pick(exp_avg_sqs), pick(max_exp_avg_sqs), pick(state_steps),
+            grad_scale, found_inf, amsgrad=amsgrad, has_complex=has_complex, beta1=beta1, beta2=beta2, lr=lr,
+            weight_decay=weight_decay, eps=eps, maximize=maximize, capturable=capturable,
+            differentiable=differentiable, decoupled_weight_decay=decoupled_weight_decay)
+        keep = [i for i, m in enumerate(mine) if m]
+        if not keep:
+            return
+        pick = lambda xs: [xs[i] for i in keep] if xs else xs  # noqa: E731
+        params, grads, exp_avgs, exp_avg_sqs = pick(params), pick(grads), pick(exp_avgs), pick(exp_avg_sqs)
+        max_exp_avg_sqs, state_steps = pick(max_exp_avg_sqs), pick(state_steps)
     beta1, beta2 = _scalar(beta1), _scalar(beta2)
     by_device: dict[torch.device, list[int]] = {}
     for i, p in enumerate(params):
-        if not p.is_cuda:
-            raise RuntimeError("pan2_amd Adam runs on HIP device tensors only; got a CPU parameter")
         by_device.setdefault(p.device, []).append(i)
     for dev, idx in by_device.items():
         pick = lambda xs: [xs[i] for i in idx]  # noqa: E731

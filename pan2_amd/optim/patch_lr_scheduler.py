@@ -1,36 +1,64 @@
 """Host-side ``LambdaLR.get_last_lr()`` for tensor learning rates.
 
-Drop-in for pan/optim/patch_lr_scheduler.py: with a tensor lr, LambdaLR keeps
-``base_lrs`` as device tensors, so reading the last lr would sync the device.
-After :func:`patch_lr_scheduler`, ``get_last_lr()`` evaluates
-``base_lr * lr_lambda(last_epoch)`` on the host from a one-time host copy of
-the base values (re-read only when ``base_lrs`` is replaced). The values the
-scheduler writes into the optimizer are unchanged.
+Drop-in for the ``patch_lr_scheduler`` of pan/optim/patch_lr_scheduler.py:38-39,
+which replaces ``LambdaLR.get_last_lr``. With a tensor lr, LambdaLR keeps
+``base_lrs`` as device tensors, and torch's ``get_last_lr()`` hands back
+device values, so every log line that reads them waits for the device.
+
+Here the base learning rates are read to the host at two fixed moments:
+when a LambdaLR is constructed and when ``load_state_dict`` replaces its
+state (both wrapped by :func:`patch_lr_scheduler`); a scheduler built before
+the patch is read once, on its first ``get_last_lr()``. ``get_last_lr()``
+then evaluates ``base * lr_lambda(last_epoch)`` from those host floats and
+never touches the device. The host copies live in a side table keyed by the
+scheduler (not in its ``__dict__``, which ``state_dict()`` serialises). The
+learning rates the scheduler writes into the optimizer are untouched.
+Assigning ``base_lrs`` directly, outside ``load_state_dict``, is not tracked.
 """
 from __future__ import annotations
 
+import functools
 from weakref import WeakKeyDictionary
 
 from torch.optim.lr_scheduler import LambdaLR
 
-# scheduler -> (the base_lrs list object, its values as python floats)
-_host_copy: "WeakKeyDictionary[LambdaLR, tuple[list, list[float]]]" = WeakKeyDictionary()
+_bases: "WeakKeyDictionary[LambdaLR, tuple[float, ...]]" = WeakKeyDictionary()
 
 
-def _host_base_lrs(sched: LambdaLR) -> list[float]:
-    entry = _host_copy.get(sched)
-    if entry is None or entry[0] is not sched.base_lrs:
-        entry = (sched.base_lrs, [float(v) for v in sched.base_lrs])
-        _host_copy[sched] = entry
-    return entry[1]
+def _capture(sched: LambdaLR) -> tuple[float, ...]:
+    """Reads the scheduler's base learning rates to the host (one device read each)."""
+    vals = tuple(float(b) for b in sched.base_lrs)
+    if len(vals) != len(sched.lr_lambdas):
+        raise ValueError(f"{len(vals)} base learning rates for {len(sched.lr_lambdas)} lr_lambdas")
+    _bases[sched] = vals
+    return vals
 
 
-def _get_last_lr_host(self: LambdaLR) -> list[float]:
-    bases = _host_base_lrs(self)
-    if len(bases) != len(self.lr_lambdas):
-        raise ValueError("base_lrs and lr_lambdas differ in length")
-    return [base * fn(self.last_epoch) for base, fn in zip(bases, self.lr_lambdas)]
+def _get_last_lr(self: LambdaLR) -> list[float]:
+    vals = _bases.get(self)
+    if vals is None:
+        vals = _capture(self)
+    epoch = self.last_epoch
+    return [b * fn(epoch) for b, fn in zip(vals, self.lr_lambdas)]
+
+
+def _wrap_once(name: str, after):
+    """Wraps LambdaLR.<name> so that after(self) runs once the original returns."""
+    orig = getattr(LambdaLR, name)
+    if getattr(orig, "_pan2_host_lr", False):
+        return
+
+    @functools.wraps(orig)
+    def wrapped(self, *args, **kwargs):
+        out = orig(self, *args, **kwargs)
+        after(self)
+        return out
+
+    wrapped._pan2_host_lr = True
+    setattr(LambdaLR, name, wrapped)
 
 
 def patch_lr_scheduler() -> None:
-    LambdaLR.get_last_lr = _get_last_lr_host
+    _wrap_once("__init__", _capture)
+    _wrap_once("load_state_dict", _capture)
+    LambdaLR.get_last_lr = _get_last_lr

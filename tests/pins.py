@@ -350,3 +350,23 @@ def check_adam_closed_form(ref):
     p2, *_ = ref.adam_step(p0, np.zeros_like(p0), np.zeros_like(p0), np.zeros_like(p0), 0.0, lr=lr, beta1=0.9,
                            beta2=0.999, eps=eps, weight_decay=0.0)
     assert np.array_equal(p2, p0)
+
+
+def check_adam_store_f16(ref):
+    """The oracle's fp16 storage rounding equals torch's own float32 -> float16
+    cast (round to nearest even) bit for bit: random values over fp16's range,
+    exact ties, overflow to inf, subnormals and NaN."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(20000) * 10.0 ** rng.uniform(-9, 4.9, 20000)).astype(np.float32)
+    one = np.float32(1.0)
+    ties = np.array([one + np.float32(2.0 ** -11), one + np.float32(3 * 2.0 ** -11), 65520.0, -65520.0, 2.0 ** -25,
+                     3 * 2.0 ** -25, 1e-8, 7e4, np.nan, np.inf, -0.0], dtype=np.float32)
+    x = np.concatenate([x, ties])
+    with np.errstate(over="ignore"):
+        got = ref._store(x, "f16")
+    want = torch.from_numpy(x).half().float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)  # NaN payloads are not compared
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))

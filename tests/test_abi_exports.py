@@ -218,7 +218,7 @@ def test_adam_argument_errors(lib):
     assert run([adam_tensor(ptrs=(FAKE, 0, FAKE, FAKE))]) == _lib.PM_EINVAL
     assert run([adam_tensor()], amsgrad=1) == _lib.PM_EINVAL
     assert "max_exp_avg_sq" in _lib.last_error()
-    assert run([adam_tensor(dts=(0, 2, 0, 0))]) == _lib.PM_EDTYPE
+    assert run([adam_tensor(dts=(0, 3, 0, 0))]) == _lib.PM_EDTYPE  # f16 (2) is accepted
     assert run([adam_tensor()], ws=0) == _lib.PM_EINVAL
     assert run([adam_tensor()], ws=FAKE + 8) == _lib.PM_EINVAL
     assert run([adam_tensor()], ws_bytes=16) == _lib.PM_EWORKSPACE

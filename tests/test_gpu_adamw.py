@@ -27,7 +27,7 @@ ADAM_MODULE = importlib.import_module("torch.optim.adam")
 
 DEV = "cuda:0"
 SIZES = [1, 7, 8, 9, 8191, 8192, 8193, 100003, 0, 64]
-DT = {"f32": torch.float32, "bf16": torch.bfloat16}
+DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def rnd(n, seed, scale=1.0):
@@ -35,6 +35,8 @@ def rnd(n, seed, scale=1.0):
 
 
 def as_dtype(x, dt):
+    if dt == "f16":
+        return x.astype(np.float16).astype(np.float32)
     return round_bf16(x) if dt == "bf16" else x
 
 
@@ -45,8 +47,9 @@ def dev(x, dt):
 def ulp(x, dt):
     """Spacing of the storage dtype at x."""
     x = np.abs(np.asarray(x, dtype=np.float32))
-    bits = 7 if dt == "bf16" else 23
-    e = np.floor(np.log2(np.maximum(x, np.float32(1e-38))))
+    bits = {"bf16": 7, "f16": 10}.get(dt, 23)
+    tiny = np.float32(2.0 ** -14) if dt == "f16" else np.float32(1e-38)  # fp16 subnormals are evenly spaced
+    e = np.floor(np.log2(np.maximum(x, tiny)))
     return np.ldexp(1.0, (e - bits).astype(int))
 
 
@@ -111,7 +114,8 @@ def test_adamw_fp32_matches_oracle_on_ragged_sizes():
 
 
 @pytest.mark.parametrize("dtypes", [("bf16", "bf16", "f32", "f32"), ("bf16", "bf16", "bf16", "bf16"),
-                                    ("f32", "bf16", "f32", "f32")])
+                                    ("f32", "bf16", "f32", "f32"), ("f16", "f16", "f16", "f16"),
+                                    ("f16", "f16", "f32", "f32")])
 def test_adamw_mixed_dtypes_match_oracle(dtypes):
     print(f"adamw dtypes {dtypes}", flush=True)
     p0s, grads = case(2, sizes=[9, 8193, 4096, 1])
@@ -197,6 +201,52 @@ def test_matches_torch_fused_adam_amsgrad_and_bf16(torch_fused_adam):
         # bf16 storage: one bf16 rounding of values that agree to a few fp32 ulps
         for a, b in ((m[i], tm[i]), (v[i], tv[i]), (x[i], tx[i]), (p[i], tp[i])):
             assert np.all(np.abs(a - b) <= ulp(b, "bf16") + 1e-6 * np.abs(b).max())
+
+
+def test_matches_torch_fused_adam_fp16(torch_fused_adam):
+    """fp16 params and state, as torch's fused Adam takes them (TORCH/optim/adam.py:803-898)."""
+    (tp, tm, tv, _, tst, _), (p, m, v, _, st, _) = _torch_vs_ours(torch_fused_adam, lr=1e-3, pdt=torch.float16)
+    assert st == tst
+    for i in range(len(p)):
+        for a, b in ((m[i], tm[i]), (v[i], tv[i]), (p[i], tp[i])):
+            assert np.all(np.abs(a - b) <= ulp(b, "f16") + 1e-6 * np.abs(b).max())
+
+
+def test_unsupported_tensors_go_to_torchs_fused_adam(torch_fused_adam):
+    """float64 device tensors and CPU tensors are left to torch's own fused Adam,
+    bit for bit what an unpatched process computes; the fp32 device tensors of
+    the same call still run on libpanmuon."""
+    from pan2_amd.optim import patch_adamw
+
+    def state(specs, seed):
+        out = []
+        for i, (dev_, dt, n) in enumerate(specs):
+            g = torch.Generator().manual_seed(seed + i)
+            p = (torch.randn(n, generator=g, dtype=torch.float64) * 0.5).to(dev_, dt)
+            out.append((p, torch.zeros_like(p), torch.zeros_like(p), torch.zeros((), device=dev_)))
+        return out
+
+    specs = [(DEV, torch.float64, 1000), ("cpu", torch.float32, 777), (DEV, torch.float32, 4096)]
+    kw = dict(amsgrad=False, has_complex=False, beta1=0.9, beta2=0.99, lr=1e-3, weight_decay=0.01, eps=1e-8,
+              maximize=False, capturable=False, differentiable=False, decoupled_weight_decay=True)
+    runs = []
+    for ours in (False, True):
+        st = state(specs, 5)
+        for k in range(2):
+            gs = [torch.full_like(p, 1e-2 * (k + 1)) for p, *_ in st]
+            lists = [list(x) for x in zip(*st)]
+            if ours:
+                patch_adamw._fused_adam(lists[0], gs, lists[1], lists[2], [], lists[3], None, None, **kw)
+            else:
+                with torch_fused_adam():
+                    ADAM_MODULE._fused_adam(lists[0], gs, lists[1], lists[2], [], lists[3], None, None, **kw)
+        torch.cuda.synchronize()
+        runs.append([[t.double().cpu() for t in s] for s in st])
+    for i in range(2):  # torch's own kernel on both sides
+        for a, b in zip(runs[0][i], runs[1][i]):
+            assert torch.equal(a, b), i
+    p_t, p_o = runs[0][2][0], runs[1][2][0]  # fp32 on the device: ours, against torch's within fp32 ulps
+    assert torch.all((p_t - p_o).abs() <= 2e-6 * p_t.abs() + 1e-9)
 
 
 def test_found_inf_skips_like_torch(torch_fused_adam):

@@ -36,9 +36,11 @@ class Tiny(torch.nn.Module):
 def restore_torch_muon():
     from torch.optim.lr_scheduler import LambdaLR
 
-    saved = (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, LambdaLR.get_last_lr)
+    saved = (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, LambdaLR.get_last_lr,
+             LambdaLR.__init__, LambdaLR.load_state_dict)
     yield
-    torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, LambdaLR.get_last_lr = saved
+    (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, LambdaLR.get_last_lr,
+     LambdaLR.__init__, LambdaLR.load_state_dict) = saved
 
 
 def test_exclusion_rules():
@@ -155,6 +157,36 @@ def test_lr_scheduler_host_get_last_lr(restore_torch_muon):
         assert got == [pytest.approx(0.1 * 0.5 ** epoch)]
         opt.step()
         sched.step()
-    # replacing base_lrs refreshes the host copy
-    sched.base_lrs = [torch.tensor(0.4)]
+    # load_state_dict re-reads the base learning rates
+    other = LambdaLR(torch.optim.SGD([torch.nn.Parameter(torch.zeros(1))], lr=torch.tensor(0.4)), lambda e: 0.5 ** e)
+    sched.load_state_dict(other.state_dict())
     assert sched.get_last_lr() == [pytest.approx(0.4 * 0.5 ** sched.last_epoch)]
+
+
+def test_lr_scheduler_reads_base_lrs_only_at_capture(restore_torch_muon):
+    """A LambdaLR built after the patch reads its base learning rates once, when
+    it is constructed: get_last_lr() never touches them again, and the host
+    copy stays out of state_dict()."""
+    from torch.optim.lr_scheduler import LambdaLR
+
+    reads = []
+
+    class Counted(float):
+        """A base lr that records every host read (float()) of itself."""
+
+        def __float__(self):
+            reads.append(1)
+            return super().__float__()
+
+    patch_lr_scheduler()
+    patch_lr_scheduler()  # idempotent
+    opt = torch.optim.SGD([torch.nn.Parameter(torch.zeros(2))], lr=Counted(0.3))
+    sched = LambdaLR(opt, [lambda e: 1.0 / (e + 1)])
+    assert reads == [1]
+    sd_keys = set(sched.state_dict())
+    for epoch in range(3):
+        assert sched.get_last_lr() == [pytest.approx(0.3 / (epoch + 1))]
+        opt.step()
+        sched.step()
+    assert reads == [1]
+    assert not any("host" in k or "pan2" in k for k in sd_keys)

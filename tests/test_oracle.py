@@ -139,3 +139,9 @@ def test_adam_closed_form():
     from oracle import adamw_ref
 
     pins.check_adam_closed_form(adamw_ref)
+
+
+def test_adam_f16_storage_matches_torch():
+    from oracle import adamw_ref
+
+    pins.check_adam_store_f16(adamw_ref)
