@@ -160,6 +160,22 @@ int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp,
                  const float* lr_dev, double lr_host,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * pm_muon_step without a caller workspace and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory while they step (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results as
+ * pm_muon_step; the workspace is a static device array of
+ * PM_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until the
+ * process ends, and the descriptor tables travel as kernel arguments. A
+ * matrix whose own workspace exceeds the scratch fails with PM_EWORKSPACE
+ * before anything is enqueued. Calls that overlap on one GPU (other threads,
+ * other streams) share its scratch and race; serialise them.
+ */
+#define PM_NOALLOC_SCRATCH_BYTES (256ull << 20)
+int pm_muon_step_noalloc(const pm_matrix* mats, int n, const pm_hparams* hp,
+                         const float* lr_dev, double lr_host, void* stream);
+
 /* Workspace needed by pm_newton_schulz. */
 size_t pm_ns_workspace_bytes(const pm_ns_matrix* mats, int n, const pm_hparams* hp);
 

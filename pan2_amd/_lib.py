@@ -37,6 +37,7 @@ EXPORTS = (
     "pm_last_error",
     "pm_workspace_bytes",
     "pm_muon_step",
+    "pm_muon_step_noalloc",
     "pm_ns_workspace_bytes",
     "pm_newton_schulz",
     "pm_momentum_nesterov",
@@ -176,6 +177,7 @@ def load() -> ctypes.CDLL:
             "pm_last_error": (ctypes.c_char_p, []),
             "pm_workspace_bytes": (sz, [pm, ctypes.c_int, php]),
             "pm_muon_step": (ctypes.c_int, [pm, ctypes.c_int, php, vp, f64, vp, sz, vp]),
+            "pm_muon_step_noalloc": (ctypes.c_int, [pm, ctypes.c_int, php, vp, f64, vp]),
             "pm_ns_workspace_bytes": (sz, [pns, ctypes.c_int, php]),
             "pm_newton_schulz": (ctypes.c_int, [pns, ctypes.c_int, php, vp, sz, vp]),
             "pm_momentum_nesterov": (ctypes.c_int, [vp, i32, vp, i32, vp, i32, i64, f32, i32, vp]),
@@ -306,14 +308,20 @@ def _step_matrices(params, grads, bufs, adj_ratios, chunks):
     return arr
 
 
+NOALLOC_SCRATCH_BYTES = 256 << 20  # PM_NOALLOC_SCRATCH_BYTES
+
+
 def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, nesterov, ns_coefficients,
-              ns_steps, eps, workspace_limit: int = 0, ns_form: str = "standard", chunks=None) -> None:
+              ns_steps, eps, workspace_limit: int = 0, ns_form: str = "standard", chunks=None,
+              noalloc: bool = False) -> None:
     """pm_muon_step over matching lists of 2-D device tensors (updated in place).
 
     lr: python float, or a 1-element float tensor on the same device (read on
     the device, no host sync). chunks: per entry, the number of equal row
     blocks orthogonalised independently (None: 1 each), addressed in place
-    without building views.
+    without building views. noalloc: call pm_muon_step_noalloc, which runs in
+    the library's static scratch (NOALLOC_SCRATCH_BYTES) with no workspace
+    tensor; workspace_limit does not apply.
     """
     lib = load()
     if len(params) == 0:
@@ -339,6 +347,11 @@ def muon_step(params, grads, bufs, adj_ratios, *, lr, weight_decay, momentum, ne
     else:
         lr_host = float(lr)
     with torch.cuda.device(dev):
+        if noalloc:
+            rc = lib.pm_muon_step_noalloc(mats, n, ctypes.byref(hp), lr_dev, lr_host, stream_of(dev))
+            check(rc, "pm_muon_step_noalloc")
+            del keep, lr_keep, arr
+            return
         nbytes = lib.pm_workspace_bytes(mats, n, ctypes.byref(hp))
         if nbytes == 0:
             check(PM_EINVAL, "pm_workspace_bytes")

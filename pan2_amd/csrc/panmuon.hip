@@ -498,8 +498,11 @@ int run_small(Launcher& L, const pm_hparams* hp) {
 // Runs one group: items[0, count) share the workspace `ws` and are all small
 // or all not.
 // How a group's descriptor table reaches the workspace: an asynchronous copy
-// from a pinned staging buffer (upload).
-enum class TablePath { kStaged };
+// from a pinned staging buffer (upload), or kernels that take it as by-value
+// arguments (load_table_by_kernel: no staging memory, for
+// pm_muon_step_noalloc).
+enum class TablePath { kStaged, kKernelArgs };
+int load_table_by_kernel(const char* src, size_t bytes, char* dst, hipStream_t stream);
 
 int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
               double lr_host, char* ws, hipStream_t stream, TablePath path) {
@@ -563,8 +566,8 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     full[i + 1] = full[i] + full_tiles(p);
     max_mp = std::max(max_mp, p.Mp);
   }
-  (void)path;
-  int rc = upload(host.data(), tb, ws, stream);
+  int rc = path == TablePath::kStaged ? upload(host.data(), tb, ws, stream)
+                                      : load_table_by_kernel(host.data(), tb, ws, stream);
   if (rc) return rc;
   timing_begin(stream);
 
@@ -737,6 +740,70 @@ int grid_for(int64_t n) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
 }
 
+// ---- the allocation-free step's descriptor tables and scratch
+
+// One launch of pm_table_load_kernel writes kTableChunk bytes of a descriptor
+// table that it receives as a kernel argument (the runtime copies kernel
+// arguments itself, so no staging memory is involved).
+constexpr int kTableChunk = 2048;
+struct TableChunk {
+  uint32_t* dst;
+  uint32_t words;  // 32-bit words of this chunk
+  uint32_t pad_;
+  uint32_t data[kTableChunk / 4];
+};
+
+__global__ __launch_bounds__(kThreads) void pm_table_load_kernel(TableChunk c) {
+  for (uint32_t i = threadIdx.x; i < c.words; i += kThreads) c.dst[i] = c.data[i];
+}
+
+int load_table_by_kernel(const char* src, size_t bytes, char* dst, hipStream_t stream) {
+  if (bytes % 4 || (uintptr_t)dst % 4) return fail(PM_EINVAL, "internal: descriptor table not in 32-bit words");
+  for (size_t off = 0; off < bytes; off += kTableChunk) {
+    TableChunk c;
+    const size_t n = std::min<size_t>(kTableChunk, bytes - off);
+    c.dst = (uint32_t*)(dst + off);
+    c.words = (uint32_t)(n / 4);
+    c.pad_ = 0;
+    std::memcpy(c.data, src + off, n);
+    hipLaunchKernelGGL(pm_table_load_kernel, dim3(1), dim3(kThreads), 0, stream, c);
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PM_OK : hip_fail(e, "descriptor table launch");
+}
+
+}  // namespace
+
+// Scratch of pm_muon_step_noalloc: the workspace of a step, held by every GPU
+// the library runs on until the process ends. Host code never uses this name
+// as an address (on the host it is only a handle for the runtime): each
+// device's own address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[PM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up on the device's first call.
+int scratch_on_device(char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(PM_EUNSUPPORTED, "device %d beyond the first %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(PM_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = (char*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -775,6 +842,30 @@ int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp, const float
   // and is rounded once, as the reference passes -adjusted_lr to its kernel.
   for (int i = 0; i < n; ++i) items[i].desc.neg_lr_host = (float)(-(lr_host * mats[i].adj_ratio));
   return run_all(items, hp, MODE_STEP, lr_dev, lr_host, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int pm_muon_step_noalloc(const pm_matrix* mats, int n, const pm_hparams* hp, const float* lr_dev, double lr_host,
+                         void* stream) {
+  g_err.clear();
+  int rc = check_hparams(hp);
+  if (rc) return rc;
+  std::vector<Item> items;
+  rc = collect_step(mats, n, hp->ns_form, items);
+  if (rc) return rc;
+  const size_t one = table_bytes(1, gemm_launches(hp));
+  for (const Item& it : items)
+    if (one + it.plan.ws > PM_NOALLOC_SCRATCH_BYTES)
+      return fail(PM_EWORKSPACE,
+                  "pm_muon_step_noalloc: a %dx%d matrix needs %zu bytes of scratch; the static scratch holds %zu "
+                  "(PM_NOALLOC_SCRATCH_BYTES); use pm_muon_step with a caller workspace",
+                  it.plan.rows, it.plan.cols, one + it.plan.ws, (size_t)PM_NOALLOC_SCRATCH_BYTES);
+  for (int i = 0; i < n; ++i) items[i].desc.neg_lr_host = (float)(-(lr_host * mats[i].adj_ratio));
+  if (items.empty()) return PM_OK;
+  char* ws = nullptr;
+  rc = scratch_on_device(&ws);
+  if (rc) return rc;
+  return run_all(items, hp, MODE_STEP, lr_dev, lr_host, ws, PM_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream,
+                 TablePath::kKernelArgs);
 }
 
 int pm_newton_schulz(const pm_ns_matrix* mats, int n, const pm_hparams* hp, void* workspace,
