@@ -148,7 +148,7 @@ def test_device_lr_matches_host_lr():
 
 
 def _torch_vs_ours(torch_fused_adam, *, lr, grad_scale=None, found_inf=None, pdt=torch.float32, amsgrad=False,
-                   decoupled=True, wd=0.05, steps=3):
+                   decoupled=True, wd=0.05, steps=3, gscale=1e-2):
     """The same steps through torch's fused Adam and through the patched one, on copies."""
     from pan2_amd.optim import patch_adamw
 
@@ -162,7 +162,7 @@ def _torch_vs_ours(torch_fused_adam, *, lr, grad_scale=None, found_inf=None, pdt
         st = [torch.zeros((), dtype=torch.float32, device=DEV) for _ in ps]
         gs_all = []
         for k in range(steps):
-            gs = [torch.from_numpy(rnd(n, 70 + 10 * k + i, 1e-2)).to(DEV, pdt) for i, n in enumerate(sizes)]
+            gs = [torch.from_numpy(rnd(n, 70 + 10 * k + i, gscale)).to(DEV, pdt) for i, n in enumerate(sizes)]
             kw = dict(amsgrad=amsgrad, has_complex=False, beta1=0.95, beta2=0.95, lr=lr, weight_decay=wd, eps=1e-8,
                       maximize=False, capturable=False, differentiable=False, decoupled_weight_decay=decoupled)
             if ours:
@@ -204,8 +204,13 @@ def test_matches_torch_fused_adam_amsgrad_and_bf16(torch_fused_adam):
 
 
 def test_matches_torch_fused_adam_fp16(torch_fused_adam):
-    """fp16 params and state, as torch's fused Adam takes them (TORCH/optim/adam.py:803-898)."""
-    (tp, tm, tv, _, tst, _), (p, m, v, _, st, _) = _torch_vs_ours(torch_fused_adam, lr=1e-3, pdt=torch.float16)
+    """fp16 params and state, as torch's fused Adam takes them (TORCH/optim/adam.py:803-898).
+    Grads of order 1 keep exp_avg_sq out of fp16's subnormal range, where the
+    spacing is so coarse that one stored ulp of difference (the two kernels
+    order their fp32 operations differently) moves sqrt(v) by tens of percent
+    on the next step; bit-exactness against the oracle covers that range."""
+    (tp, tm, tv, _, tst, _), (p, m, v, _, st, _) = _torch_vs_ours(torch_fused_adam, lr=1e-3, pdt=torch.float16,
+                                                                  gscale=1.0)
     assert st == tst
     for i in range(len(p)):
         for a, b in ((m[i], tm[i]), (v[i], tv[i]), (p[i], tp[i])):
