@@ -46,6 +46,29 @@ PM_HD void full_tile(int lt, int np, int nq, int& ti, int& tj) {
   tj = r / gm;
 }
 
+// The same np x nq grid walked column group by column group: kGroupCols
+// columns at a time, and within a column group kGroupRows rows at a time
+// (each such block column by column), so the kXcds blocks that run at once go
+// down the rows of the same columns. For C = S·X, whose right operand (Xᵀ
+// panels, one per tile column) is the large one, the XCDs then read the same
+// few column panels at the same time and the memory-side cache serves the
+// repeats: each panel comes from HBM about once instead of once per row group.
+constexpr int kGroupCols = 8;
+
+PM_HD void full_tile_cols(int lt, int np, int nq, int& ti, int& tj) {
+  const int per_cg = kGroupCols * np;  // tiles of a full column group
+  const int cg = lt / per_cg;
+  const int c0 = cg * kGroupCols;
+  const int cw = imin(kGroupCols, nq - c0);
+  const int r = lt - cg * per_cg;
+  const int rg = r / (kGroupRows * cw);
+  const int g0 = rg * kGroupRows;
+  const int gm = imin(kGroupRows, np - g0);
+  const int w = r - rg * kGroupRows * cw;
+  ti = g0 + w % gm;
+  tj = c0 + w / gm;
+}
+
 // Upper triangle (ti <= tj) of an nt x nt tile grid, grouped the same way;
 // lt in [0, nt*(nt+1)/2).
 PM_HD void sym_tile(int lt, int nt, int& ti, int& tj) {

@@ -10,12 +10,15 @@ int main() {
   int bad = 0;
   for (int np = 1; np <= 130; ++np) {
     for (int nq = 1; nq <= 130; nq += (nq < 20 ? 1 : 7)) {
-      std::vector<int> seen(np * nq, 0);
-      for (int lt = 0; lt < np * nq; ++lt) {
-        int ti, tj;
-        pm::full_tile(lt, np, nq, ti, tj);
-        if (ti < 0 || ti >= np || tj < 0 || tj >= nq || seen[ti * nq + tj]++) {
-          if (bad++ < 5) std::printf("full np=%d nq=%d lt=%d -> (%d,%d)\n", np, nq, lt, ti, tj);
+      for (int walk = 0; walk < 2; ++walk) {
+        std::vector<int> seen(np * nq, 0);
+        for (int lt = 0; lt < np * nq; ++lt) {
+          int ti, tj;
+          if (walk == 0) pm::full_tile(lt, np, nq, ti, tj);
+          else pm::full_tile_cols(lt, np, nq, ti, tj);
+          if (ti < 0 || ti >= np || tj < 0 || tj >= nq || seen[ti * nq + tj]++) {
+            if (bad++ < 5) std::printf("full%s np=%d nq=%d lt=%d -> (%d,%d)\n", walk ? "_cols" : "", np, nq, lt, ti, tj);
+          }
         }
       }
     }
