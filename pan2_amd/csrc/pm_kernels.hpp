@@ -641,6 +641,80 @@ __device__ __forceinline__ void load_quads(u16x4 (&v)[kQuads], const uint16_t* _
   }
 }
 
+// Per-wave staging of 16 rows x 128 bytes (2 KiB of LDS) that turns the
+// accumulator layout into full-line global stores. A wave's 128 x 64 sub-tile
+// is 64 columns wide, one 128-byte line per row in either workspace layout
+// (its column runs start at multiples of 64), so each store instruction can
+// write 8 whole rows: lane l writes bytes 16(l%8)..16(l%8)+15 of row 8s + l/8.
+// The quads land in the slot as they sit in registers; chunk c (16 bytes) of
+// staged row r is kept at chunk c ^ swz(r), with the swizzle chosen per
+// orientation so that the quad writes hit distinct banks (32-byte runs per row
+// for the normal orientation, 16-byte runs for the transposed one); the
+// row-order read-back is conflict-free under either. Only the wave itself
+// touches its slot, and LDS executes one wave's accesses in order, so no
+// barrier is needed between a round's writes and reads or between rounds.
+constexpr int kStageBytes = 16 * 128;
+__device__ __forceinline__ int swz_norm(int r) { return ((r >> 1) & 3) << 1; }
+__device__ __forceinline__ int swz_tr(int r) { return (r >> 1) & 7; }
+
+// Normal orientation: quads o[ni] (rows 4g + r, column 16 ni + lane%16) of
+// one 16-row band; after quad_transpose lane l holds row 4g + l%4, columns
+// 16 ni + 4 c4 .. + 3 (g = l/16, c4 = (l%16)/4).
+__device__ __forceinline__ void stage_band(char* slot, const u16x4 (&o)[kNi], int lane) {
+  const int r = 4 * (lane >> 4) + (lane & 3), c4 = (lane & 15) >> 2;
+#pragma unroll
+  for (int ni = 0; ni < kNi; ++ni) {
+    const int c = 2 * ni + (c4 >> 1);
+    *(u16x4*)(slot + r * 128 + ((c ^ swz_norm(r)) << 4) + ((c4 & 1) << 3)) = quad_transpose(o[ni], lane);
+  }
+}
+
+// Transposed orientation: the quads of four consecutive 16-row bands mi at one
+// 16-column block ni, staged as 16 rows (columns 16 ni + lane%16 of the tile)
+// of 64 elements (rows 16 mi + 4g + r): lane l's quad is 8 consecutive bytes
+// of staged row l%16.
+__device__ __forceinline__ void stage_block_tr(char* slot, const u16x4 (&o)[4], int lane) {
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = 2 * m + (g >> 1);
+    *(u16x4*)(slot + r * 128 + ((c ^ swz_tr(r)) << 4) + ((g & 1) << 3)) = o[m];
+  }
+}
+
+// Writes the 16 staged rows to memory, row r to row_at(r) (the row's first
+// element of the 64-column run), 8 whole rows per store instruction.
+template <bool TR, class RowAt>
+__device__ __forceinline__ void stage_flush(const char* slot, int lane, RowAt&& row_at) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int r = 8 * s + (lane >> 3), c = lane & 7;
+    const u32x4 v = *(const u32x4*)(slot + r * 128 + ((c ^ (TR ? swz_tr(r) : swz_norm(r))) << 4));
+    *(u32x4*)(row_at(r) + 8 * c) = v;
+  }
+}
+
+// load_quads for the band group hb only (bands mi = 4hb .. 4hb+3): v[m * kNi + ni].
+__device__ __forceinline__ void load_quads_half(u16x4 (&v)[kQuads / 2], const uint16_t* __restrict__ T, int64_t ld,
+                                                bool tiled, int pbase, int qbase, int lane, int hb) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const int g1 = (lane >> 4) & 1;
+  u32x4 w[kQuads / 4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int ni = 0; ni < kNi; ni += 2)
+      w[(m * kNi + ni) / 2] =
+          *(const u32x4*)(T + ws_off(qbase + (ni + g1) * 16, pbase + (4 * hb + m) * 16 - 4 * g1, ld, tiled));
+#pragma unroll
+  for (int k = 0; k < kQuads / 4; ++k) {
+    const auto s0 = __builtin_amdgcn_permlane16_swap(w[k].x, w[k].z, false, false);
+    const auto s1 = __builtin_amdgcn_permlane16_swap(w[k].y, w[k].w, false, false);
+    v[2 * k] = __builtin_bit_cast(u16x4, (u32x2){s0[0], s1[0]});
+    v[2 * k + 1] = __builtin_bit_cast(u16x4, (u32x2){s0[1], s1[1]});
+  }
+}
+
 // Register vector of 4 param elements of the FINAL epilogue.
 template <bool F32> struct PickVec { typedef u16x4 type; typedef uint16_t elem; };
 template <> struct PickVec<true> { typedef f32x4 type; typedef float elem; };
@@ -693,9 +767,10 @@ __device__ __forceinline__ int xcc_id() {
 // keeps the epilogue's registers within budget); other stages ignore it.
 // AX_IN_ACC (FINAL): the caller has already added a·X to the accumulators
 // (acc = a·x + acc, the same fp32 operations), so X is not read again.
+// slot: this wave's staging slot (kStageBytes of LDS) for GRAM, SYMM and UPDATE.
 template <int STAGE, int PDT, int LAYOUT, bool AX_IN_ACC = false, class D>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, const TileJob& job,
-                                              const f32x4 (&acc)[kMi][kNi], int wave) {
+                                              const f32x4 (&acc)[kMi][kNi], int wave, char* slot = nullptr) {
 #pragma clang fp contract(off)
   const int cur = args.cur;
   constexpr bool tx = LAYOUT & kTiledX, ts = LAYOUT & kTiledS;
@@ -719,15 +794,64 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
     // their transposes). A GRAM diagonal tile is bitwise symmetric already
     // (the same products in the same order), and so is SYMM's when L == R.
     const bool diag = STAGE == ST_SYMM && !mirror;
-    u16x4 av[kQuads];
-    if (STAGE == ST_SYMM) {
-      // the addend is symmetric, so its quads can be read from either orientation
-      if (cb != 0.0f) {
-        load_quads(av, d.S[args.sd], ldc, ts, pbase, qbase, lane);
-      } else {
+    if (ts && !diag) {
+      // full tiles: staged full-line stores, normal orientation and (off the
+      // diagonal) the mirror, band group by band group; the addend (symmetric,
+      // so read from either orientation) a band group at a time
+      const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
+      // both halves of the addend are loaded before any store, so neither
+      // load waits behind stores in vmcnt order
+      u16x4 ahv[2][kQuads / 2];
 #pragma unroll
-        for (int i = 0; i < kQuads; ++i) av[i] = (u16x4){0, 0, 0, 0};
+      for (int hb = 0; hb < 2; ++hb) {
+        if (STAGE == ST_SYMM && cb != 0.0f) {
+          load_quads_half(ahv[hb], d.S[args.sd], ldc, ts, pbase, qbase, lane, hb);
+        } else {
+#pragma unroll
+          for (int i = 0; i < kQuads / 2; ++i) ahv[hb][i] = (u16x4){0, 0, 0, 0};
+        }
       }
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const u16x4 (&ah)[kQuads / 2] = ahv[hb];
+        u16x4 o[4][kNi];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int ni = 0; ni < kNi; ++ni) {
+            const int mi = 4 * hb + m, i = m * kNi + ni;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float x = acc[mi][ni][r];
+              o[m][ni][r] = f2bf((STAGE == ST_GRAM) ? x * s : cc * x + cb * bf2f(ah[i][r]));
+            }
+          }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          stage_band(slot, o[m], lane);
+          const int p0 = pw + (4 * hb + m) * 16;
+          stage_flush<false>(slot, lane, [&](int r) { return C + ws_off(p0 + r, qw, ldc, ts); });
+        }
+        if (mirror) {
+#pragma unroll
+          for (int ni = 0; ni < kNi; ++ni) {
+            const u16x4 blk[4] = {o[0][ni], o[1][ni], o[2][ni], o[3][ni]};
+            stage_block_tr(slot, blk, lane);
+            const int p0 = pw + 64 * hb;
+            stage_flush<true>(slot, lane, [&](int r) { return C + ws_off(qw + 16 * ni + r, p0, ldc, ts); });
+          }
+        }
+      }
+      return;
+    }
+    // diagonal SYMM tiles (masked element stores of the upper part and its
+    // mirror), and the row-major outputs of pm_gram / pm_gemm_symmetric
+    u16x4 av[kQuads];
+    if (STAGE == ST_SYMM && cb != 0.0f) {
+      load_quads(av, d.S[args.sd], ldc, ts, pbase, qbase, lane);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kQuads; ++i) av[i] = (u16x4){0, 0, 0, 0};
     }
     const int g1 = (lane >> 4) & 1;
 #pragma unroll
@@ -778,22 +902,33 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
       for (int i = 0; i < kQuads; ++i) xv[i] = (u16x4){0, 0, 0, 0};
     }
-    const int g1 = (lane >> 4) & 1;
+    // X' and X'ᵀ through the staging slot, band group by band group
+    const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
 #pragma unroll
-    for (int mi = 0; mi < kMi; ++mi)
+    for (int hb = 0; hb < 2; ++hb) {
+      u16x4 o[4][kNi];
 #pragma unroll
-      for (int ni = 0; ni < kNi; ni += 2) {
-        const int p0 = pbase + mi * 16;
-        u16x4 o[2];
+      for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int i = mi * kNi + ni + h, q = qbase + (ni + h) * 16;
+        for (int ni = 0; ni < kNi; ++ni) {
+          const int mi = 4 * hb + m, i = mi * kNi + ni;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[h][r] = f2bf((ca * bf2f(xv[i][r]) + acc[mi][ni + h][r]) * s);
-          *(u16x4*)(Xn + ws_off(p0 + (lane & 3), q & ~3, ldx, tx)) = quad_transpose(o[h], lane);
+          for (int r = 0; r < 4; ++r) o[m][ni][r] = f2bf((ca * bf2f(xv[i][r]) + acc[mi][ni][r]) * s);
         }
-        *(u32x4*)(XTn + ws_off(qbase + (ni + g1) * 16, p0 - 4 * g1, ldxt, tx)) = pair_rows(o[0], o[1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        stage_band(slot, o[m], lane);
+        const int p0 = pw + (4 * hb + m) * 16;
+        stage_flush<false>(slot, lane, [&](int r) { return Xn + ws_off(p0 + r, qw, ldx, tx); });
       }
+#pragma unroll
+      for (int ni = 0; ni < kNi; ++ni) {
+        const u16x4 blk[4] = {o[0][ni], o[1][ni], o[2][ni], o[3][ni]};
+        stage_block_tr(slot, blk, lane);
+        const int p0 = pw + 64 * hb;
+        stage_flush<true>(slot, lane, [&](int r) { return XTn + ws_off(qw + 16 * ni + r, p0, ldxt, tx); });
+      }
+    }
     return;
   }
 
@@ -903,6 +1038,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   __shared__ __attribute__((aligned(1024))) char lds_a1[kOpBytes];
   __shared__ __attribute__((aligned(1024))) char lds_b0[kOpBytes];
   __shared__ __attribute__((aligned(1024))) char lds_b1[kOpBytes];
+  __shared__ __attribute__((aligned(16))) char lds_stage[kGemmThreads / 64][kStageBytes];
   __shared__ int s_tile[2];
   __shared__ int s_home;
   const Ring ring{{lds_a0, lds_a1}, {lds_b0, lds_b1}};
@@ -951,7 +1087,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     const bool leader = wave == 0 && lane_id() == 0;
     int after = -1;
     if (leader && tn >= 0) after = grab_tile(args.queues, total, &s_home);
-    gemm_epilogue<STAGE, PDT, LAYOUT>(args, descs[m], job, acc, wave);
+    gemm_epilogue<STAGE, PDT, LAYOUT>(args, descs[m], job, acc, wave, lds_stage[wave]);
     if (leader) s_tile[slot ^ 1] = after;
     if (tn < 0) break;
     t = tn;
