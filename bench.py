@@ -214,6 +214,41 @@ def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
     return 0
 
 
+def probe_ceiling(units: int = 3000) -> int:
+    """MFMA ceilings of the GEMM engine's loop on this chip (pan2_amd/csrc/pm_probe.hip):
+    MFMA alone, MFMA with the engine's LDS fragment reads and barriers, and the
+    same with 4 waves of 128 x 128; one line each."""
+    import ctypes
+
+    import torch
+
+    from pan2_amd.build import PROBE_LIB
+
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    lib = ctypes.CDLL(PROBE_LIB)
+    fn = lib.pp_ceiling
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
+                   ctypes.POINTER(ctypes.c_double)]
+    out = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    names = {0: "mfma only (8 waves of 128x64 accumulators, register operands)",
+             1: "mfma + LDS fragment reads + 2 barriers per 64-deep unit (8 waves of 128x64)",
+             2: "mfma + LDS fragment reads + 2 barriers per 64-deep unit (4 waves of 128x128)"}
+    for which in (0, 1, 2, 0, 1, 2):
+        ms, fl = ctypes.c_float(), ctypes.c_double()
+        torch.cuda.synchronize()
+        rc = fn(which, cus, units if which != 2 else units // 2, ctypes.c_void_p(out.data_ptr()), ctypes.byref(ms),
+                ctypes.byref(fl))
+        if rc != 0:
+            print(f"probe ceiling {which}: failed", file=sys.stderr)
+            return 1
+        tf = fl.value / (ms.value * 1e-3) / 1e12
+        print(f"probe ceiling {which}: {tf:.1f} TFLOP/s = {100 * tf / PEAK_BF16_TFLOPS:.1f}% of {PEAK_BF16_TFLOPS} "
+              f"({ms.value:.3f} ms) -- {names[which]}", flush=True)
+    return 0
+
+
 def hbm_stream(device, mib: int = 2048, reps: int = 5) -> dict:
     """What plain streams reach on this box's HBM, beside the 8 TB/s peak the
     HBM rooflines are quoted against: torch's device copy (mib MiB read + mib
@@ -380,13 +415,16 @@ def main() -> int:
                          "per GEMM launch (needs --fetch-csv, --write-csv, --copy-mib)")
     ap.add_argument("--fetch-csv")
     ap.add_argument("--write-csv")
-    ap.add_argument("--probe", choices=("ns", "bmm"),
+    ap.add_argument("--probe", choices=("ns", "bmm", "ceiling"),
                     help="counter probe instead of the Muon step: 'ns' runs Newton-Schulz alone on 16 x 5120^2 "
                          "bf16 matrices through pm_newton_schulz, 'bmm' the same 16 x 5120^3 products through "
-                         "torch.bmm (hipBLASLt) for comparison")
+                         "torch.bmm (hipBLASLt) for comparison; 'ceiling' the MFMA ceilings of the engine's loop "
+                         "(pan2_amd/csrc/pm_probe.hip)")
     args = ap.parse_args()
     if args.traffic_summary:
         return traffic_summary(args)
+    if args.probe == "ceiling":
+        return probe_ceiling()
     if args.probe:
         return probe(args.probe)
     if args.gpus != 1:

@@ -37,10 +37,11 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> str:
-    """Compile csrc/panmuon.hip into pan2_amd/libpanmuon.so; returns the path."""
-    src = os.path.join(CSRC, "panmuon.hip")
-    tmp = LIB + ".tmp"
+PROBE_LIB = os.path.join(HERE, "libpanprobe.so")
+
+
+def _compile(src: str, out: str, verbose: bool) -> None:
+    tmp = out + ".tmp"
     cmd = [hipcc(), *HIPCC_FLAGS, src, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -49,7 +50,15 @@ def build(verbose: bool = False) -> str:
         noise = "packed-fp32-ops"
         err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile csrc/panmuon.hip into pan2_amd/libpanmuon.so (and the ceiling
+    probes of csrc/pm_probe.hip, measurement only, into libpanprobe.so);
+    returns the library's path."""
+    _compile(os.path.join(CSRC, "panmuon.hip"), LIB, verbose)
+    _compile(os.path.join(CSRC, "pm_probe.hip"), PROBE_LIB, verbose)
     return LIB
 
 
