@@ -954,6 +954,69 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   }
   const bool step = args.mode == MODE_STEP;
   constexpr bool f32p = PDT == DT_F32;  // MODE_NS launches the bf16 instantiation
+  if (!f32p && slot) {
+    // bf16 params: when this wave's 64 param rows x 128 columns lie inside the
+    // param and rows are 16-byte aligned, the bf16 update goes through the
+    // staging slot 16 rows x 64 columns at a time, and the param is read,
+    // stepped and written as full lines (the same fp32 operations per element)
+    const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
+    const bool whole = qw + kWaveCols <= prow && pw + kWaveRows <= pcol && ldp % 8 == 0 &&
+                       (uintptr_t)d.param % 16 == 0;
+    if (whole) {
+      uint16_t* P = (uint16_t*)d.param;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        __builtin_amdgcn_sched_barrier(0);
+        u16x4 xh[4][kNi];
+        u32x4 pv[kNi][2];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int ni = 0; ni < kNi; ++ni)
+            xh[m][ni] = (!AX_IN_ACC && ca != 0.0f)
+                            ? *(const u16x4*)(T + ws_off(qbase + ni * 16, pbase + (4 * hb + m) * 16, ldt, tx))
+                            : (u16x4){0, 0, 0, 0};
+#pragma unroll
+        for (int ni = 0; ni < kNi; ++ni)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            pv[ni][h] = step ? *(const u32x4*)(P + (int64_t)(qw + 16 * ni + 8 * h + (lane >> 3)) * ldp + pw + 64 * hb +
+                                               8 * (lane & 7))
+                             : (u32x4){0, 0, 0, 0};
+#pragma unroll
+        for (int ni = 0; ni < kNi; ++ni) {
+          u16x4 blk[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = acc[4 * hb + m][ni][e];
+              blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xh[m][ni][e]) + a) * s);  // bf16 update
+            }
+          stage_block_tr(slot, blk, lane);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int r = 8 * h + (lane >> 3), c = lane & 7;
+            const u32x4 on = *(const u32x4*)(slot + r * 128 + ((c ^ swz_tr(r)) << 4));
+            u32x4 out;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              uint16_t o2[2];
+#pragma unroll
+              for (int half = 0; half < 2; ++half) {
+                const float onv = bf2f((uint16_t)(on[k] >> (16 * half)));
+                const float pe = bf2f((uint16_t)(pv[ni][h][k] >> (16 * half)));
+                o2[half] = f2bf(step ? pe * wdf + onv * neg : onv);
+              }
+              out[k] = (uint32_t)o2[0] | ((uint32_t)o2[1] << 16);
+            }
+            *(u32x4*)(P + (int64_t)(qw + 16 * ni + r) * ldp + pw + 64 * hb + 8 * c) = out;
+          }
+        }
+      }
+      return;
+    }
+  }
   const int vec_align = f32p ? 16 : 8;
   const bool vec = (ldp % 4 == 0) && ((uintptr_t)d.param % vec_align == 0);
   // Bands of kNi quads (16 tile rows = kNi param rows x 4 columns each) are
