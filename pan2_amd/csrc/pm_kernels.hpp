@@ -682,15 +682,57 @@ __device__ __forceinline__ void stage_block_tr(char* slot, const u16x4 (&o)[4], 
   }
 }
 
-// Writes the 16 staged rows to memory, row r to row_at(r) (the row's first
-// element of the 64-column run), 8 whole rows per store instruction.
-template <bool TR, class RowAt>
-__device__ __forceinline__ void stage_flush(const char* slot, int lane, RowAt&& row_at) {
+// Writes the 16 staged rows to memory, row r to row0 + r·step (row0: the
+// first element of the block's 64-column run; step: 64 in the panel layout,
+// whose 16-row blocks never cross a panel, or ld row-major), 8 whole rows per
+// store instruction.
+// The stores are buffer stores off a resource for the block (its base is
+// wave-uniform, so only a 32-bit offset per lane lives in vector registers).
+template <bool TR>
+__device__ __forceinline__ void stage_flush(const char* slot, int lane, uint16_t* row0, int step) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(row0, (short)0, (15 * step + 64) * 2, 0x00020000);
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int r = 8 * s + (lane >> 3), c = lane & 7;
     const u32x4 v = *(const u32x4*)(slot + r * 128 + ((c ^ (TR ? swz_tr(r) : swz_norm(r))) << 4));
-    *(u32x4*)(row_at(r) + 8 * c) = v;
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, (r * step + 8 * c) * 2, 0, 0);
+  }
+}
+
+// Quads T[q][p..p+3] of a wave's band group as full-line loads: round ni
+// covers rows q = qw + 16 ni + 0..15 and columns p = p0 .. p0 + 63 (p0 a
+// multiple of 64), lane l loading 16 bytes of row 8h + l/8 at column
+// p0 + 8 (l % 8) into raw[ni][h]. unstage_quads turns one round into the
+// quads of the accumulator layout through the wave's staging slot.
+// The 64 rows qw .. qw+63 (qw a multiple of 64) lie in one 256-row panel, so
+// in the panel layout they are 64 elements apart, and ld apart row-major.
+__device__ __forceinline__ void load_rounds(u32x4 (&raw)[kNi][2], const uint16_t* __restrict__ T, int64_t ld,
+                                            bool tiled, int qw, int p0, int lane) {
+  const int step = tiled ? 64 : (int)ld;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(T + ws_off(qw, p0, ld, tiled)), (short)0, (63 * step + 64) * 2, 0x00020000);
+  const int v0 = ((lane >> 3) * step + 8 * (lane & 7)) * 2;
+#pragma unroll
+  for (int ni = 0; ni < kNi; ++ni)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      raw[ni][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, v0 + (16 * ni + 8 * h) * step * 2, 0, 0));
+}
+
+// Writes round raw[2] to the slot in the transposed staging layout and reads
+// back quad m = 0..3 of this lane: T[q][p0 + 16m + 4g .. + 3] for q = the
+// round's row lane % 16 (g = lane / 16), the layout stage_block_tr writes.
+__device__ __forceinline__ void unstage_quads(char* slot, const u32x4 (&raw)[2], u16x4 (&q)[4], int lane) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 8 * h + (lane >> 3), c = lane & 7;
+    *(u32x4*)(slot + r * 128 + ((c ^ swz_tr(r)) << 4)) = raw[h];
+  }
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = 2 * m + (g >> 1);
+    q[m] = *(const u16x4*)(slot + r * 128 + ((c ^ swz_tr(r)) << 4) + ((g & 1) << 3));
   }
 }
 
@@ -713,6 +755,14 @@ __device__ __forceinline__ void load_quads_half(u16x4 (&v)[kQuads / 2], const ui
     v[2 * k] = __builtin_bit_cast(u16x4, (u32x2){s0[0], s1[0]});
     v[2 * k + 1] = __builtin_bit_cast(u16x4, (u32x2){s0[1], s1[1]});
   }
+}
+
+// d.scales[i] through the constant address space: a scalar load (the norm
+// kernel wrote it in an earlier launch, and a launch starts with its scalar
+// cache invalidated), so no vector register holds the address or the value.
+template <class D>
+__device__ __forceinline__ float scale_of(const D& d, int i) {
+  return ((const __attribute__((address_space(4))) float*)d.scales)[i];
 }
 
 // Register vector of 4 param elements of the FINAL epilogue.
@@ -785,7 +835,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   if (STAGE == ST_GRAM || STAGE == ST_SYMM) {
     uint16_t* C = d.S[args.sc];
     const int64_t ldc = d.Mp;
-    const float s = (STAGE == ST_GRAM && args.first) ? d.scales[0] : 1.0f;
+    const float s = (STAGE == ST_GRAM && args.first) ? scale_of(d, 0) : 1.0f;
     const float cb = args.b, cc = args.c;
     const bool mirror = job.ti != job.tj;
     // A diagonal tile of L·Rᵀ with L != R is symmetric only up to rounding:
@@ -799,38 +849,36 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
       // diagonal) the mirror, band group by band group; the addend (symmetric,
       // so read from either orientation) a band group at a time
       const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
-      // both halves of the addend are loaded before any store, so neither
-      // load waits behind stores in vmcnt order
-      u16x4 ahv[2][kQuads / 2];
+      // the addend (symmetric, so read in the transposed orientation) as
+      // full-line loads; each band group's loads are issued before the
+      // previous group's stores, so no load waits behind stores in vmcnt order
+      const bool addend = STAGE == ST_SYMM && cb != 0.0f;
+      u32x4 raw[kNi][2];
+      if (addend) load_rounds(raw, d.S[args.sd], ldc, ts, qw, pw, lane);
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
-        if (STAGE == ST_SYMM && cb != 0.0f) {
-          load_quads_half(ahv[hb], d.S[args.sd], ldc, ts, pbase, qbase, lane, hb);
-        } else {
-#pragma unroll
-          for (int i = 0; i < kQuads / 2; ++i) ahv[hb][i] = (u16x4){0, 0, 0, 0};
-        }
-      }
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        const u16x4 (&ah)[kQuads / 2] = ahv[hb];
         u16x4 o[4][kNi];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int ni = 0; ni < kNi; ++ni) {
+          u16x4 ah[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+          if (addend) unstage_quads(slot, raw[ni], ah, lane);
 #pragma unroll
-          for (int ni = 0; ni < kNi; ++ni) {
-            const int mi = 4 * hb + m, i = m * kNi + ni;
+          for (int m = 0; m < 4; ++m) {
+            const int mi = 4 * hb + m;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float x = acc[mi][ni][r];
-              o[m][ni][r] = f2bf((STAGE == ST_GRAM) ? x * s : cc * x + cb * bf2f(ah[i][r]));
+              o[m][ni][r] = f2bf((STAGE == ST_GRAM) ? x * s : cc * x + cb * bf2f(ah[m][r]));
             }
           }
+        }
+        // the second band group's addend is requested before this group's stores
+        if (hb == 0 && addend) load_rounds(raw, d.S[args.sd], ldc, ts, qw, pw + 64, lane);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           stage_band(slot, o[m], lane);
           const int p0 = pw + (4 * hb + m) * 16;
-          stage_flush<false>(slot, lane, [&](int r) { return C + ws_off(p0 + r, qw, ldc, ts); });
+          stage_flush<false>(slot, lane, C + ws_off(p0, qw, ldc, ts), ts ? 64 : (int)ldc);
         }
         if (mirror) {
 #pragma unroll
@@ -838,7 +886,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
             const u16x4 blk[4] = {o[0][ni], o[1][ni], o[2][ni], o[3][ni]};
             stage_block_tr(slot, blk, lane);
             const int p0 = pw + 64 * hb;
-            stage_flush<true>(slot, lane, [&](int r) { return C + ws_off(qw + 16 * ni + r, p0, ldc, ts); });
+            stage_flush<true>(slot, lane, C + ws_off(qw + 16 * ni, p0, ldc, ts), ts ? 64 : (int)ldc);
           }
         }
       }
@@ -889,44 +937,46 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
     return;
   }
 
-  const float s = args.first ? d.scales[1] : 1.0f;
+  const float s = args.first ? scale_of(d, 1) : 1.0f;
   const float ca = args.a;
   if (STAGE == ST_UPDATE) {
     uint16_t* Xn = d.X[cur ^ 1];
     uint16_t* XTn = d.XT[cur ^ 1];
     const int64_t ldx = d.Np, ldxt = d.Mp;
-    u16x4 xv[kQuads];
-    if (ca != 0.0f) {
-      load_quads(xv, d.XT[cur], ldxt, tx, pbase, qbase, lane);  // X[p][q] = Xᵀ[q][p]
-    } else {
-#pragma unroll
-      for (int i = 0; i < kQuads; ++i) xv[i] = (u16x4){0, 0, 0, 0};
-    }
-    // X' and X'ᵀ through the staging slot, band group by band group
+    // X[p][q] = Xᵀ[q][p] as full-line loads of Xᵀ (each band group's loads
+    // issued before the previous group's stores); X' and X'ᵀ go out through
+    // the staging slot
     const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
+    u32x4 raw[kNi][2];
+    if (ca != 0.0f) load_rounds(raw, d.XT[cur], ldxt, tx, qw, pw, lane);
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
       u16x4 o[4][kNi];
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
+      for (int ni = 0; ni < kNi; ++ni) {
+        u16x4 xq[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+        if (ca != 0.0f) unstage_quads(slot, raw[ni], xq, lane);
 #pragma unroll
-        for (int ni = 0; ni < kNi; ++ni) {
-          const int mi = 4 * hb + m, i = mi * kNi + ni;
+        for (int m = 0; m < 4; ++m) {
+          const int mi = 4 * hb + m;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[m][ni][r] = f2bf((ca * bf2f(xv[i][r]) + acc[mi][ni][r]) * s);
+          for (int r = 0; r < 4; ++r) o[m][ni][r] = f2bf((ca * bf2f(xq[m][r]) + acc[mi][ni][r]) * s);
         }
+      }
+      // the second band group's X is requested before this group's stores
+      if (hb == 0 && ca != 0.0f) load_rounds(raw, d.XT[cur], ldxt, tx, qw, pw + 64, lane);
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         stage_band(slot, o[m], lane);
         const int p0 = pw + (4 * hb + m) * 16;
-        stage_flush<false>(slot, lane, [&](int r) { return Xn + ws_off(p0 + r, qw, ldx, tx); });
+        stage_flush<false>(slot, lane, Xn + ws_off(p0, qw, ldx, tx), tx ? 64 : (int)ldx);
       }
 #pragma unroll
       for (int ni = 0; ni < kNi; ++ni) {
         const u16x4 blk[4] = {o[0][ni], o[1][ni], o[2][ni], o[3][ni]};
         stage_block_tr(slot, blk, lane);
         const int p0 = pw + 64 * hb;
-        stage_flush<true>(slot, lane, [&](int r) { return XTn + ws_off(qw + 16 * ni + r, p0, ldxt, tx); });
+        stage_flush<true>(slot, lane, XTn + ws_off(qw + 16 * ni, p0, ldxt, tx), tx ? 64 : (int)ldxt);
       }
     }
     return;
