@@ -1017,15 +1017,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
         __builtin_amdgcn_sched_barrier(0);
-        u16x4 xh[4][kNi];
+        // X (rows = param rows) as full-line loads, transposed into quads through the slot
+        const bool ax = !AX_IN_ACC && ca != 0.0f;
+        u32x4 xr[kNi][2];
+        if (ax) load_rounds(xr, T, ldt, tx, qw, pw + 64 * hb, lane);
         u32x4 pv[kNi][2];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-          for (int ni = 0; ni < kNi; ++ni)
-            xh[m][ni] = (!AX_IN_ACC && ca != 0.0f)
-                            ? *(const u16x4*)(T + ws_off(qbase + ni * 16, pbase + (4 * hb + m) * 16, ldt, tx))
-                            : (u16x4){0, 0, 0, 0};
 #pragma unroll
         for (int ni = 0; ni < kNi; ++ni)
 #pragma unroll
@@ -1035,13 +1031,15 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
                              : (u32x4){0, 0, 0, 0};
 #pragma unroll
         for (int ni = 0; ni < kNi; ++ni) {
+          u16x4 xq[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+          if (ax) unstage_quads(slot, xr[ni], xq, lane);
           u16x4 blk[4];
 #pragma unroll
           for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float a = acc[4 * hb + m][ni][e];
-              blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xh[m][ni][e]) + a) * s);  // bf16 update
+              blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xq[m][e]) + a) * s);  // bf16 update
             }
           stage_block_tr(slot, blk, lane);
 #pragma unroll
