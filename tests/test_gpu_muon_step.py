@@ -8,6 +8,9 @@ exceeds that bound, no more than 1.25x torch's own max |Δparam| (measured in
 the test). On the config-1 shape torch's bf16 path lands at ~1.44e-3·lr: the
 elementwise spread of any bf16 NS there is larger than 1e-3·lr.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -16,6 +19,7 @@ import torch.optim._muon as torch_muon
 from oracle import muon_ref
 from pan2_amd.optim.muon import build_native_muon_optimizers
 from pan2_amd.optim.patch_muon import patch_muon
+from tests.test_gpu_full_size import band
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -76,9 +80,22 @@ def test_step_config1_gate(patched, adjust):
     _, u = muon_ref.momentum_nesterov(b, g, 0.95)
     o_t = TORCH_ZEROPOWER(torch.from_numpy(u).to(DEV), (3.4445, -4.7750, 2.0315), 5, 1e-7).float().cpu().numpy()
     dp_torch = float(np.abs(muon_ref.step_param(p0, o_t, lr, 0.01, ratio) - ref_p).max())
+    sv = np.linalg.svd(o_got, compute_uv=False)
+    lo, hi = band(*shape)  # closed-form band: the quintic over the Marchenko-Pastur support
+    band_ok = bool(lo - 0.03 <= sv.min() and sv.max() <= hi + 0.03)
     print(f"  rel-Frobenius(O)={err:.3e} max|dp|/adj_lr={dp / (lr * ratio):.3e} "
-          f"torch-bf16 max|dp|/adj_lr={dp_torch / (lr * ratio):.3e}")
+          f"torch-bf16 max|dp|/adj_lr={dp_torch / (lr * ratio):.3e} sigma [{sv.min():.4f}, {sv.max():.4f}]")
+    log = os.environ.get("PM_FULL_STEP_LOG")
+    if log:  # the same record as tests/test_gpu_full_step.py writes for configs 2-5
+        with open(log, "a") as f:
+            f.write(json.dumps({"config": 1, "matrix": 0, "shape": list(shape), "adjust_lr_fn": adjust,
+                                "param_dtype": "torch.float32", "rel_fro": err, "readout_rel_bound": 0.0,
+                                "sigma_min": float(sv.min()), "sigma_max": float(sv.max()), "band": [lo, hi],
+                                "band_ok": band_ok, "max_dp_over_lr": dp / lr, "max_dp_over_adj_lr": dp / (lr * ratio),
+                                "torch_bf16_max_dp_over_adj_lr": dp_torch / (lr * ratio),
+                                "north_star_dp_met": dp <= 1e-3 * lr}) + "\n")
     assert err <= 2e-2
+    assert band_ok
     assert dp <= max(1e-3 * lr * ratio, 1.25 * dp_torch)
 
 
