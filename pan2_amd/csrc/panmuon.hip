@@ -159,7 +159,7 @@ int32_t sym_tiles(const Plan& p) {
   return nt * (nt + 1) / 2;
 }
 int32_t full_tiles(const Plan& p) {
-  return p.small ? (p.Np + kSmApplyCols - 1) / kSmApplyCols : (p.Mp / kTile) * (p.Np / kTile);
+  return p.small ? p.Np / kSmApplyCols : (p.Mp / kTile) * (p.Np / kTile);
 }
 
 // One matrix of a call, whatever the entry point.
@@ -380,7 +380,7 @@ struct Launcher {
     GemmArgs a = ga;
     a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = 0; a.a = coef_a; a.cur = cur; a.first = first;
     a.prefix = full; a.total = full_total;
-    const dim3 grid(full_total), block(kSmApplyThreads);
+    const dim3 grid(full_grid), block(kSmApplyThreads);  // persistent: one block per CU
     if (last && final_f32)
       hipLaunchKernelGGL((pm_small_apply_kernel<ST_FINAL, DT_F32>), grid, block, 0, stream, a);
     else if (last)

@@ -12,11 +12,13 @@
 //                            _gram_newtonschulz_local (pan/optim/patch_muon.py:
 //                            320-331): Z = c R² + b R; Q = a I + Z, then
 //                            Q Z + a Q; R <- Z (R Z + a R) + a (R Z + a R); S = Q
-//   pm_small_apply_kernel  X' = s·(a·X + S X) over 128 x 512 tiles with the
-//                          arithmetic of the grouped engine's UPDATE / FINAL
-//                          (X', or the fused parameter step). Small matrices
-//                          keep X only, no Xᵀ: the apply reads X transposed
-//                          from LDS.
+//   pm_small_apply_kernel  X' = s·(a·X + S X) with the arithmetic of the
+//                          grouped engine's UPDATE / FINAL (X', or the fused
+//                          parameter step): one persistent block per CU
+//                          streams 64-column units of X (and, for the step,
+//                          their param blocks) through an LDS ring across
+//                          matrices. Small matrices keep X only, no Xᵀ: the
+//                          apply reads X transposed from LDS.
 //
 // This is the counterpart of the reference's fused batched gram-NS
 // (pan/optim/muon_triton.py:234-345: the gram and the 128 x 128 iteration in
@@ -36,10 +38,9 @@ constexpr int kSmMat = kSm * kSmRow;  // 32 KiB: one 128 x 128 bf16 matrix
 constexpr int kSmUnit = kSm * 128;    // 16 KiB: 128 rows x 64 k values, one gram unit
 constexpr int kSmRing = 8;            // gram units in LDS: 7 in flight while one is read (gram form)
 constexpr int kSmRingStd = 4;         // standard form: 64 KiB of ring, two blocks per CU
-constexpr int kSmApplyWaves = 8;                     // apply blocks: waves of 128 x 64
+constexpr int kSmApplyWaves = 8;      // apply blocks: 8 waves, each 64 rows x 16 columns of a unit
 constexpr int kSmApplyThreads = 64 * kSmApplyWaves;
-constexpr int kSmApplyCols = 64 * kSmApplyWaves;     // columns of X per apply tile: one 1 KiB row
-static_assert(kSmApplyCols * 2 == 1024, "an apply tile row is one 1 KiB copy");
+constexpr int kSmApplyCols = 64;      // columns of X per apply work item: one 16 KiB unit
 
 struct SmallCoreArgs {
   const MatDesc* descs;
@@ -361,18 +362,13 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
   }
 }
 
-// Chunk c16 of row r of a flat LDS array of 256-byte rows, swizzled as in SmMat.
-__device__ __forceinline__ int sm_off(int r, int c16) { return r * kSmRow + ((c16 ^ (r & 15)) << 4); }
-
-// The X tile of an apply block in LDS, laid out as X is in HBM (sm_x_off):
-// kSmApplyCols / 64 units of 64 columns (n), each kSm rows (k) of 128 B.
-// Chunk c (16 B, columns 8c .. 8c+7 of the unit) of row k is stored at chunk
-// c ^ (2·((k >> 3) & 3)): the transposed fragment reads (16 consecutive
-// columns of rows k, k+8, k+16, k+24 in one instruction) then fall in 32
-// distinct banks.
-constexpr int kSmXUnits = kSmApplyCols / 64;  // units per tile
+// A unit of X in LDS, laid out as in HBM (sm_x_off): kSm rows (k) of 64
+// columns (n), 128 B each. Chunk c (16 B, columns 8c .. 8c+7) of row k is
+// stored at chunk c ^ (2·((k >> 3) & 3)): the transposed fragment reads (16
+// consecutive columns of rows k, k+8, k+16, k+24 in one instruction) then fall
+// in 32 distinct banks.
 __device__ __forceinline__ int xt_off(int k, int n) {
-  return (n >> 6) * kSmUnit + k * 128 + ((((n >> 3) & 7) ^ (((k >> 3) & 3) << 1)) << 4) + (n & 7) * 2;
+  return k * 128 + ((((n >> 3) & 7) ^ (((k >> 3) & 3) << 1)) << 4) + (n & 7) * 2;
 }
 
 // Param elements r, c0 .. c0+3 of a small matrix's FINAL: whether the row is
@@ -416,206 +412,402 @@ __device__ __forceinline__ void store_param4(const MatDesc& d, const Quad4& q, c
   }
 }
 
-// X' = s·(a·X + S X) for one tile of kSmApplyCols columns of a small matrix
-// per block (prefix: ceil(Np / kSmApplyCols) tiles per matrix). Small
-// matrices keep X only (no Xᵀ): the X tile, 128 contiguous KiB of HBM in the
-// panel layout (sm_x_off), is copied into LDS in that layout, and the MFMA's
-// B fragments (8 consecutive k of one column) are read from it transposed,
-// element by element. Each wave owns a 128 x 64 wave tile. The arithmetic is
-// the grouped engine's UPDATE / FINAL (the same MFMA over the same k order,
-// the same rounding points), so the result equals the engine's on the
-// zero-padded matrix; only the stores differ: X' alone (no Xᵀ copy), and the
-// parameter step in param layout for wide and tall matrices alike.
+// ---- the apply: X' = s·(a·X + S X), or the FINAL parameter step, streamed
+// unit by unit.
+//
+// One persistent block per CU walks a contiguous range of the launch's units
+// (64 columns of one matrix's X: 16 contiguous KiB in the panel layout;
+// prefix: Np / 64 units per matrix), matrix after matrix. The units stream
+// through an LDS ring as the core kernel's gram does: while one unit is
+// multiplied, the copies of the next kRing - 2 are in flight, so the block's
+// loads never stop for its products or stores. FINAL with a parameter step
+// copies the unit's param block (128 x 64 param elements) into the same slot.
+// S = the matrix's 128 x 128 product from the core kernel; each wave keeps
+// the fragments of its 64 rows of S in registers (loaded when the walk enters
+// a matrix). Wave w owns rows 64(w%2) .. +63 and columns 16(w/2) .. +15 of
+// the unit's S X; a wide FINAL computes the same elements transposed (Xᵀ S,
+// whose quads are param rows), a tall one steps param rows directly.
+//
+// The products are the grouped engine's UPDATE / FINAL element for element
+// (the same MFMA over the same k order, bf16 rounding at the same points, the
+// same fp32 step), so the result equals the engine's on the zero-padded matrix.
+template <int STAGE, int PDT>
+struct SmApply {
+  static constexpr bool kFinal = STAGE == ST_FINAL;
+  static constexpr bool kF32 = PDT == DT_F32;
+  static constexpr int kEsz = kF32 ? 4 : 2;
+  static constexpr int kRing = kFinal ? (kF32 ? 3 : 4) : 8;      // slots
+  static constexpr int kPBytes = kFinal ? kSm * 64 * kEsz : 16;  // a unit's param block
+  static constexpr int kXCopies = kSmUnit / 1024 / kSmApplyWaves;
+  static constexpr int kPCopies = kFinal ? kPBytes / 1024 / kSmApplyWaves : 0;
+  static constexpr int kCopies = kXCopies + kPCopies;  // 1 KiB copies per unit and wave
+  static constexpr int kStores = 4;                    // vector stores per unit and wave
+  // vmcnt while waiting for the r-th unit of the block: the copies of the
+  // kRing - 2 units issued after its own, and the stores of the units since
+  // (copies are issued right after each unit's barrier, its stores last)
+  static constexpr int kWaitMax = (kRing - 2) * kCopies + (kRing - 1) * kStores;
+  static_assert(kWaitMax < 64, "vmcnt range");
+  static_assert(kRing * (kSmUnit + (kFinal ? kPBytes : 0)) <= 160 * 1024, "LDS");
+};
+
+// Waits for the copies of the r-th unit of a block (r counted from 0).
+template <class C, int R = 0>
+__device__ __forceinline__ void wait_unit(int r) {
+  if constexpr (R < C::kRing - 1) {
+    if (r == R) {
+      wait_vmcnt<(C::kRing - 2) * C::kCopies + R * C::kStores>();
+      return;
+    }
+    wait_unit<C, R + 1>(r);
+  } else {
+    wait_vmcnt<C::kWaitMax>();
+  }
+}
+
+// One 16-byte-per-lane LDS-DMA copy, and the buffer stores of the apply's
+// param step (functions rather than builtins in the kernel's lambdas, which
+// are host-device and must not name target builtins directly).
+__device__ __forceinline__ void sm_copy(__amdgpu_buffer_rsrc_t rs, char* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(dst), 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void sm_store(__amdgpu_buffer_rsrc_t rs, int off, const float (&v)[4]) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, (f32x4){v[0], v[1], v[2], v[3]}), rs, off, 0, 0);
+}
+__device__ __forceinline__ void sm_store_bf16(__amdgpu_buffer_rsrc_t rs, int off, const float (&v)[4]) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 pk = {(uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
+                    (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16)};
+  __builtin_amdgcn_raw_buffer_store_b64(pk, rs, off, 0, 0);
+}
+
+struct SmSlots {
+  char* x[8];
+  char* p[4];
+};
+
+// Position of a walk over the launch's units: matrix m, its unit lu of nu.
+struct SmWalk {
+  int m, lu, nu;
+};
+
+typedef const __attribute__((address_space(4))) MatDesc* SmDescPtr;
+typedef const __attribute__((address_space(4))) int32_t* SmPrefixPtr;
+
+// A unit's param block: rows of RB bytes, chunk c (16 B) of row r stored at
+// chunk c ^ (r & 7) (128-byte rows) or c ^ (r & 15) (wider rows).
+template <int RB>
+__device__ __forceinline__ int pb_off(int r, int byte) {
+  constexpr int kSwz = RB == 128 ? 7 : 15;
+  return r * RB + ((((byte >> 4) ^ (r & kSwz))) << 4) + (byte & 15);
+}
+
 template <int STAGE, int PDT>
 __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(1024))) char sbuf[kSm * kSmRow];       // S, 32 KiB
-  __shared__ __attribute__((aligned(1024))) char xbuf[kSmXUnits * kSmUnit];  // X tile, 128 KiB
-  const int t = blockIdx.x;
-  const int m = find_matrix(args.prefix, args.n, t);
-  const MatDesc& d = args.descs[m];
-  const int lt = t - args.prefix[m];
-  const int w = wave_id(), lane = lane_id();
-  const int Np = __builtin_amdgcn_readfirstlane(d.Np);
-  const int n0 = lt * kSmApplyCols;
-  const int nx = min(kSmApplyCols, Np - n0);  // columns of this tile inside X
-  const uint16_t* X = d.X[args.cur];
-  {
-    // S: copy q moves rows 4q .. 4q+3 (1 KiB); lane l lands at row 4q + l/16,
-    // stored chunk l%16, so it loads logical chunk (l%16) ^ ((4q + l/16) & 15)
-    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(d.S[args.sl], (uint32_t)kSm * kSmRow);
-    const int row = lane >> 4;
-    for (int q = w; q < kSm / 4; q += kSmApplyWaves) {
-      const int voff = row * kSmRow + (((lane & 15) ^ ((4 * q + row) & 15)) << 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(sbuf + q * 1024), 16, voff, q * 4 * kSmRow, 0, 0);
-    }
-    // X tile: the tile's units are contiguous in HBM (sm_x_off; n0 is a
-    // multiple of 64). Wave w moves unit w, the 64 columns its S X products
-    // read: copy i moves rows 8i .. 8i+7 (1 KiB); lane l lands at row 8i + l/8,
-    // stored chunk l%8, so it loads logical chunk (l%8) ^ swizzle(row). Units
-    // past Np read as zeros (buffer bounds).
-    static_assert(kSmXUnits == kSmApplyWaves, "one unit of the X tile per wave");
-    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(X + sm_x_off(0, n0), (uint32_t)(nx / 64) * kSmUnit);
-#pragma unroll
-    for (int i = 0; i < kSm / 8; ++i) {
-      const int k = 8 * i + (lane >> 3);
-      const int lc = (lane & 7) ^ (((k >> 3) & 3) << 1);  // logical chunk of row k
-      const int voff = 64 * w < nx ? w * kSmUnit + k * 128 + lc * 16 : 0x7fffffff;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(xbuf + w * kSmUnit + i * 1024), 16, voff, 0, 0, 0);
-    }
+  typedef SmApply<STAGE, PDT> C;
+  constexpr bool kFinal = C::kFinal, kF32 = C::kF32;
+  constexpr int kRing = C::kRing, kEsz = C::kEsz;
+  typedef typename PickVec<kF32>::type PV;
+  typedef typename PickVec<kF32>::elem PE;
+  // the ring: one __shared__ array per slot, so the compiler's LDS-DMA
+  // tracking sees that reads of one slot do not wait for copies into another
+  SmSlots sl = {};
+  __shared__ __attribute__((aligned(1024))) char x0[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char x1[kSmUnit];
+  __shared__ __attribute__((aligned(1024))) char x2[kSmUnit];
+  sl.x[0] = x0; sl.x[1] = x1; sl.x[2] = x2;
+  if constexpr (kRing >= 4) {
+    __shared__ __attribute__((aligned(1024))) char x3[kSmUnit];
+    sl.x[3] = x3;
   }
-  // S is shared: every wave's S copies (issued before its X copies) land
-  // before the block barrier. X is not: a wave waits for its own unit only,
-  // except in the wide FINAL, whose waves read two units each. Bare barriers:
-  // __syncthreads' fence would wait for every copy in flight.
-  wait_vmcnt<kSm / 8>();
-  block_barrier();
-  wait_vmcnt<0>();
-  if (STAGE == ST_FINAL && !d.trans) block_barrier();
-  const int r16 = lane & 15, g = lane >> 4;
-  // the MFMA fragment of X column n for k-step s (k = 32s + 8g .. +7), read
-  // transposed from the tile, element by element
-  auto xcol = [&](int s, int n) {
-    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-    u16x8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = *(const uint16_t*)(xbuf + xt_off(32 * s + 8 * g + e, n));
-    return __builtin_bit_cast(bf16x8, v);
-  };
-  f32x4 acc[kMi][kNi];
-#pragma unroll
-  for (int i = 0; i < kMi; ++i)
-#pragma unroll
-    for (int j = 0; j < kNi; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  if (STAGE == ST_FINAL && !d.trans) {
-    // wide FINAL: the transposed tile X'ᵀ = Xᵀ Sᵀ, whose quads are param rows,
-    // finished by the grouped engine's FINAL epilogue. Wave w owns Xᵀ rows
-    // (columns n of X) xr .. xr+127, xr = 128(w/2), and S rows 64(w%2) .. +63.
-    const int xr = 128 * (w >> 1);
-    if (xr >= nx) return;  // past Np: no barrier follows
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8 b[kNi];
-#pragma unroll
-      for (int j = 0; j < kNi; ++j) b[j] = *(const bf16x8*)(sbuf + sm_off(64 * (w & 1) + 16 * j + r16, 4 * s + g));
-#pragma unroll
-      for (int i = 0; i < kMi; ++i) {
-        const bf16x8 a = xcol(s, xr + 16 * i + r16);
-#pragma unroll
-        for (int j = 0; j < kNi; ++j) acc[i][j] = mfma_bf16(a, b[j], acc[i][j]);
-      }
-    }
-    const int xg = n0 + xr;  // first n of the wave
-    TileJob job{};
-    job.ti = xg / kTile;
-    job.tj = 0;
-    const int ew = ((xg % kTile) / kWaveRows) * 4 + (w & 1);  // the engine wave whose quads these are
-    if (args.a != 0.0f) {
-      // a·X from the tile in LDS rather than from HBM: quad (i, j) is
-      // Xᵀ[xr + 16i + 4g .. +3][m], m = 64(w%2) + 16j + lane%16, i.e. 4
-      // consecutive columns of X row m; acc = a·x + acc as the engine's epilogue
-      // forms it
-      const float ca = args.a;
-#pragma unroll
-      for (int i = 0; i < kMi; ++i)
-#pragma unroll
-        for (int j = 0; j < kNi; ++j) {
-          const u16x4 xq = *(const u16x4*)(xbuf + xt_off(64 * (w & 1) + 16 * j + r16, xr + 16 * i + 4 * g));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] = ca * bf2f(xq[r]) + acc[i][j][r];
-        }
-      gemm_epilogue<ST_FINAL, PDT, 0, true>(args, d, job, acc, ew);
-    } else {
-      gemm_epilogue<ST_FINAL, PDT, 0>(args, d, job, acc, ew);  // a = 0: X is not read
-    }
-    return;
+  if constexpr (kRing == 8) {
+    __shared__ __attribute__((aligned(1024))) char x4[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char x5[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char x6[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char x7[kSmUnit];
+    sl.x[4] = x4; sl.x[5] = x5; sl.x[6] = x6; sl.x[7] = x7;
   }
-  // S X: wave w owns columns xr .. xr+63 of the tile (B = X, read transposed), all 128 rows (A = S)
-  const int xr = 64 * w;
-  if (xr >= nx) return;  // past Np: no barrier follows
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    bf16x8 b[kNi];
-#pragma unroll
-    for (int j = 0; j < kNi; ++j) b[j] = xcol(s, xr + 16 * j + r16);
-#pragma unroll
-    for (int i = 0; i < kMi; ++i) {
-      const bf16x8 a = *(const bf16x8*)(sbuf + sm_off(16 * i + r16, 4 * s + g));
-#pragma unroll
-      for (int j = 0; j < kNi; ++j) acc[i][j] = mfma_bf16(a, b[j], acc[i][j]);
+  if constexpr (kFinal) {
+    __shared__ __attribute__((aligned(1024))) char p0[C::kPBytes];
+    __shared__ __attribute__((aligned(1024))) char p1[C::kPBytes];
+    __shared__ __attribute__((aligned(1024))) char p2[C::kPBytes];
+    sl.p[0] = p0; sl.p[1] = p1; sl.p[2] = p2;
+    if constexpr (kRing >= 4) {
+      __shared__ __attribute__((aligned(1024))) char p3[C::kPBytes];
+      sl.p[3] = p3;
     }
   }
 
-  // ---- epilogue: o = bf16(s·(a·X + S X)) at rows p0 .. p0+3 of column q per quad
-  const float sc = args.first ? d.scales[1] : 1.0f;
+  const SmDescPtr descs = (SmDescPtr)args.descs;
+  const SmPrefixPtr prefix = (SmPrefixPtr)args.prefix;
+  const int u0 = (int)((int64_t)blockIdx.x * args.total / gridDim.x);
+  const int u1 = (int)((int64_t)(blockIdx.x + 1) * args.total / gridDim.x);
+  if (u0 >= u1) return;
+  const int w = wave_id(), lane = lane_id();
+  const int r16 = lane & 15, g = lane >> 4;
+  const int wr = w & 1, wc = w >> 1;  // rows 64·wr .. +63, columns 16·wc .. +15 of the unit
+  const bool step = kFinal && args.mode == MODE_STEP;
   const float ca = args.a;
-  // the o quad of (i, j), in the accumulator layout
-  auto quad_o = [&](int i, int j, u16x4& o) {
-    const int pr = 16 * i + 4 * g + (lane & 3);
-    const int q4 = (xr + 16 * j + r16) & ~3;
-    u16x4 xq = (u16x4){0, 0, 0, 0};
-    if (ca != 0.0f)  // X[pr][q4 .. q4+3] from the tile, then to the quad layout
-      xq = quad_transpose(*(const u16x4*)(xbuf + xt_off(pr, q4)), lane);
+  float lr = 0.0f;
+  if (step && args.lr_dev) lr = *args.lr_dev;
+
+  SmWalk cw;  // the copy walk, kRing - 1 units ahead of the compute walk
+  cw.m = find_matrix(prefix, args.n, u0);
+  cw.lu = u0 - prefix[cw.m];
+  cw.nu = prefix[cw.m + 1] - prefix[cw.m];
+  SmWalk kw = cw;
+  int cu = u0;  // the unit the copy walk issues next
+
+  // lane offsets of this wave's X copies: copy q = kXCopies·w + h moves rows
+  // 8q .. 8q+7 of the unit; lane l lands at row 8q + l/8, stored chunk l%8, so
+  // it loads logical chunk (l%8) ^ 2·(q%4)
+  int xvo[C::kXCopies];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = f2bf((ca * bf2f(xq[r]) + acc[i][j][r]) * sc);
-  };
-  if (STAGE == ST_UPDATE) {
-    uint16_t* Xn = d.X[args.cur ^ 1];
-#pragma unroll
-    for (int i = 0; i < kMi; ++i)
-#pragma unroll
-      for (int j = 0; j < kNi; ++j) {
-        u16x4 o;
-        quad_o(i, j, o);
-        const int pr = 16 * i + 4 * g + (lane & 3), q4 = (xr + 16 * j + r16) & ~3;
-        *(u16x4*)(Xn + sm_x_off(pr, n0 + q4)) = quad_transpose(o, lane);  // row pr, columns q4 .. +3
-      }
-    return;
+  for (int h = 0; h < C::kXCopies; ++h) {
+    const int q = C::kXCopies * w + h;
+    xvo[h] = (8 * q + (lane >> 3)) * 128 + (((lane & 7) ^ ((q & 3) << 1)) << 4);
   }
-  // FINAL of a tall matrix (a wide one returned above): param row n0 + q,
-  // columns p0 .. p0+3, o as it is. Param loads go out kBatch rows of quads
-  // at a time, before any of them is combined.
-  constexpr bool f32p = PDT == DT_F32;
-  constexpr int kBatch = f32p ? 2 : 4;
-  const bool step = args.mode == MODE_STEP;
-  float wdf = 0.0f, neg = 0.0f;
-  if (step) {
-    if (args.lr_dev) {
-      const float lr = *args.lr_dev;
-      wdf = 1.0f - lr * args.wd;
-      neg = -(lr * d.adj_ratio);
+
+  // Issues the copies of the copy walk's unit into slot S (zero-length
+  // copies past the block's range, so every unit issues kCopies per wave),
+  // then advances the walk.
+  auto issue = [&](char* xs, char* ps) {
+    const bool live = cu < u1;
+    const int m = live ? cw.m : 0;
+    auto& d = descs[m];
+    const uint16_t* xb = d.X[args.cur] + sm_x_off(0, 64 * cw.lu);
+    const __amdgpu_buffer_rsrc_t rx = uniform_rsrc(xb, live ? (uint32_t)kSmUnit : 0u);
+#pragma unroll
+    for (int h = 0; h < C::kXCopies; ++h) {
+      const int q = C::kXCopies * w + h;
+      sm_copy(rx, xs + q * 1024, xvo[h]);
+    }
+    if constexpr (kFinal) {
+      // the param block: rows of RB bytes (wide: 128 param rows x 64 columns;
+      // tall: 64 param rows x 128 columns), copied only for a step whose
+      // param rows are 16-byte aligned (else its units take the masked path)
+      const bool wide = !d.trans;
+      const int64_t ld = d.p_ld;
+      const bool dma = live && step && (ld * kEsz) % 16 == 0 && ((uintptr_t)d.param & 15) == 0;
+      const int64_t row0 = wide ? 0 : 64 * (int64_t)cw.lu, col0 = wide ? 64 * (int64_t)cw.lu : 0;
+      const PE* pb = (const PE*)d.param + row0 * ld + col0;
+      // valid bytes from pb: up to the param's last element
+      const int64_t valid = (((int64_t)d.rows - 1 - row0) * ld + d.cols - col0) * kEsz;
+      const uint32_t nrec = !dma || valid <= 0 ? 0u : valid >= 0x7fffffff ? 0x7fffffffu : (uint32_t)valid;
+      const __amdgpu_buffer_rsrc_t rp = uniform_rsrc((const uint16_t*)pb, nrec);
+      const int rb = (wide ? 64 : 128) * kEsz;  // row bytes: 128, 256 or 512
+      const int lpr = rb / 16;                   // lanes per row
+#pragma unroll
+      for (int h = 0; h < C::kPCopies; ++h) {
+        const int q = C::kPCopies * w + h;
+        const int r = q * (1024 / rb) + lane / lpr, c = lane % lpr;
+        const int lc = c ^ (r & (rb == 128 ? 7 : 15));
+        const int voff = (int)((int64_t)r * ld * kEsz) + lc * 16;
+        sm_copy(rp, ps + q * 1024, voff);
+      }
+    }
+    if (live && ++cw.lu == cw.nu) {
+      ++cw.m;
+      cw.lu = 0;
+      if (cw.m < args.n) cw.nu = prefix[cw.m + 1] - prefix[cw.m];
+    }
+    ++cu;
+  };
+
+  // per-matrix state of the compute walk: this wave's S fragments (rows
+  // 64wr + 16i + lane%16, k = 32s + 8g .. +7) and the scalars of the matrix
+  bf16x8 sa[4][4];
+  float sc = 1.0f, neg = 0.0f;
+  auto enter = [&](int m) {
+    auto& d = descs[m];
+    const uint16_t* S = d.S[args.sl];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        sa[i][s] = *(const bf16x8*)(S + (64 * wr + 16 * i + r16) * kSm + 32 * s + 8 * g);
+    sc = args.first ? d.scales[1] : 1.0f;
+    if (step) neg = args.lr_dev ? -(lr * d.adj_ratio) : d.neg_lr_host;
+    // the fragments complete in order behind every copy in flight: wait for
+    // all of them here, so that no unit after this one waits for them again
+    wait_vmcnt<0>();
+  };
+  const float wdf = step ? (args.lr_dev ? 1.0f - lr * args.wd : args.wdf_host) : 0.0f;
+
+  // prologue: the first kRing - 1 units
+#pragma unroll
+  for (int s = 0; s < kRing - 1; ++s) issue(sl.x[s], sl.p[s & 3]);
+  enter(kw.m);
+
+  // one unit in slot S: wait for its copies, release slot S-1 to the copy
+  // walk, multiply, store
+  auto unit = [&](char* xs, const char* ps, char* nxs, char* nps, int u) {
+    wait_unit<C>(u - u0);
+    block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
+    if (kw.lu == kw.nu) {  // the walk enters the next matrix
+      ++kw.m;
+      kw.lu = 0;
+      kw.nu = prefix[kw.m + 1] - prefix[kw.m];
+      enter(kw.m);
+    }
+    issue(nxs, nps);
+    auto& d = descs[kw.m];
+    const int n0 = 64 * kw.lu;  // the unit's first column of X
+    const bool wide = kFinal && !d.trans;
+    // the MFMA fragment of X column n for k-step s (k = 32s + 8g .. +7), read
+    // transposed from the unit, element by element; for these k the swizzle
+    // of xt_off is (n/8 % 8) ^ 2g whatever s and e are
+    auto xcol = [&](int s, int n) {
+      typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+      const char* base = xs + 8 * g * 128 + ((((n >> 3) & 7) ^ (2 * g)) << 4) + (n & 7) * 2;
+      u16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = *(const uint16_t*)(base + (32 * s + e) * 128);
+      return __builtin_bit_cast(bf16x8, v);
+    };
+    f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (wide) {
+      // Xᵀ S: acc[i] = rows n = 16wc + 4g .. +3 (of Xᵀ) of column m = 64wr + 16i + lane%16
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 xa = xcol(s, 16 * wc + r16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = mfma_bf16(xa, sa[i][s], acc[i]);
+      }
     } else {
-      wdf = args.wdf_host;
-      neg = d.neg_lr_host;
+      // S X: acc[i] = rows m = 64wr + 16i + 4g .. +3 of column n = 16wc + lane%16
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 xb = xcol(s, 16 * wc + r16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = mfma_bf16(sa[i][s], xb, acc[i]);
+      }
+    }
+    ++kw.lu;
+    // ---- the bf16 update o = bf16(s·(a·X + ...)) of quad i, in the accumulator layout
+    u16x4 o[4];
+    if (wide) {
+      // quad i is X[m][n .. n+3] transposed: m = 64wr + 16i + lane%16, n =
+      // 16wc + 4g; acc = a·x + acc as the engine's FINAL epilogue forms it
+      // (with a = 0 it adds a·0 = +0, which turns a -0 accumulator into +0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u16x4 xq = (u16x4){0, 0, 0, 0};
+        if (ca != 0.0f) xq = *(const u16x4*)(xs + xt_off(64 * wr + 16 * i + r16, 16 * wc + 4 * g));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[i][e] = f2bf((ca * bf2f(xq[e]) + acc[i][e]) * sc);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // X[pr][q4 .. q4+3] from the unit, then to the quad layout
+        const int pr = 64 * wr + 16 * i + 4 * g + (lane & 3), q4 = (16 * wc + r16) & ~3;
+        u16x4 xq = (u16x4){0, 0, 0, 0};
+        if (ca != 0.0f) xq = quad_transpose(*(const u16x4*)(xs + xt_off(pr, q4)), lane);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[i][e] = f2bf((ca * bf2f(xq[e]) + acc[i][e]) * sc);
+      }
+    }
+    if constexpr (!kFinal) {
+      // X' row pr, columns n0 + q4 .. +3
+      uint16_t* xn = d.X[args.cur ^ 1] + sm_x_off(0, n0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pr = 64 * wr + 16 * i + 4 * g + (lane & 3), q4 = (16 * wc + r16) & ~3;
+        *(u16x4*)(xn + pr * 64 + q4) = quad_transpose(o[i], lane);
+      }
+      return;
+    }
+    // ---- FINAL: quad i is param row pr, columns pc .. pc+3 (relative to the
+    // unit's param block): wide pr = 64wr + 16i + lane%16, pc = 16wc + 4g;
+    // tall pr = 16wc + lane%16, pc = 64wr + 16i + 4g
+    const int64_t ld = d.p_ld;
+    const int64_t row0 = wide ? 0 : n0, col0 = wide ? n0 : 0;
+    const int rows = d.rows - (int)row0, cols = d.cols - (int)col0;  // of the block, from its corner
+    PE* pbase = (PE*)d.param + row0 * ld + col0;
+    const bool aligned = ld % 4 == 0 && ((uintptr_t)d.param % sizeof(PV)) == 0 &&
+                         (!step || ((ld * kEsz) % 16 == 0 && ((uintptr_t)d.param & 15) == 0));
+    const bool regular = aligned && (wide ? cols >= 64 : d.cols % 4 == 0) && (int64_t)kSm * ld * kEsz < 0x7fffffff;
+    auto prow = [&](int i) { return wide ? 64 * wr + 16 * i + r16 : 16 * wc + r16; };
+    auto pcol = [&](int i) { return wide ? 16 * wc + 4 * g : 64 * wr + 16 * i + 4 * g; };
+    auto stepped = [&](int i, const PV& pv, float (&v)[4]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pe = kF32 ? (float)pv[e] : bf2f((uint16_t)pv[e]);
+        v[e] = step ? pe * wdf + bf2f(o[i][e]) * neg : bf2f(o[i][e]);
+      }
+    };
+    if (regular) {
+      // param values from the block in LDS; one buffer store per quad, those
+      // outside the param dropped by the buffer's range
+      const int64_t valid = ((int64_t)d.rows - 1 - row0) * ld * kEsz + (int64_t)cols * kEsz;
+      const uint32_t nrec = valid <= 0 ? 0u : valid >= 0x7fffffff ? 0x7fffffffu : (uint32_t)valid;
+      const __amdgpu_buffer_rsrc_t rs = uniform_rsrc((const uint16_t*)pbase, nrec);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = prow(i), c = pcol(i);
+        PV pv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pv[e] = 0;
+        if (step)
+          pv = wide ? *(const PV*)(ps + pb_off<64 * kEsz>(r, c * kEsz)) : *(const PV*)(ps + pb_off<128 * kEsz>(r, c * kEsz));
+        float v[4];
+        stepped(i, pv, v);
+        const bool in = r < rows && c < cols;
+        const int off = in ? (int)((int64_t)r * ld * kEsz) + c * kEsz : -16;  // -16: past any range
+        if constexpr (kF32)
+          sm_store(rs, off, v);
+        else
+          sm_store_bf16(rs, off, v);
+      }
+      return;
+    }
+    // at the param's edges, or rows not 16-byte aligned: element by element
+    // from and to the param, then every memory operation of the block is
+    // waited for, so the copy waits above stay exact
+    const MatDesc& dl = args.descs[kw.m];  // (generic address space for the helpers)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const Quad4 qd = quad4_at<kF32>(dl, (int)row0 + prow(i), (int)col0 + pcol(i));
+      PV pv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = 0;
+      if (step) pv = load_param4<kF32>(dl, qd);
+      float v[4];
+      stepped(i, pv, v);
+      store_param4<kF32>(dl, qd, v);
+    }
+    wait_vmcnt<0>();
+  };
+
+  // slot S holds unit u0 + S (mod kRing); unit S releases slot S - 1 to the copy walk
+#define PM_SM_UNIT(S)                                                                                 \
+  unit(sl.x[S], sl.p[(S) & 3], sl.x[((S) + kRing - 1) % kRing], sl.p[(((S) + kRing - 1) % kRing) & 3], u + (S))
+  for (int u = u0; u < u1; u += kRing) {
+    PM_SM_UNIT(0);
+    if (u + 1 >= u1) break;
+    PM_SM_UNIT(1);
+    if (u + 2 >= u1) break;
+    PM_SM_UNIT(2);
+    if constexpr (kRing >= 4) {
+      if (u + 3 >= u1) break;
+      PM_SM_UNIT(3);
+    }
+    if constexpr (kRing == 8) {
+      if (u + 4 >= u1) break;
+      PM_SM_UNIT(4);
+      if (u + 5 >= u1) break;
+      PM_SM_UNIT(5);
+      if (u + 6 >= u1) break;
+      PM_SM_UNIT(6);
+      if (u + 7 >= u1) break;
+      PM_SM_UNIT(7);
     }
   }
-#pragma unroll
-  for (int i0 = 0; i0 < kMi; i0 += kBatch) {
-    __builtin_amdgcn_sched_barrier(0);
-    typename PickVec<f32p>::type pv[kBatch][kNi];
-#pragma unroll
-    for (int bi = 0; bi < kBatch; ++bi)
-#pragma unroll
-      for (int j = 0; j < kNi; ++j) {
-        const Quad4 qd = quad4_at<f32p>(d, n0 + xr + 16 * j + r16, 16 * (i0 + bi) + 4 * g);
-        if (step) pv[bi][j] = load_param4<f32p>(d, qd);
-      }
-#pragma unroll
-    for (int bi = 0; bi < kBatch; ++bi)
-#pragma unroll
-      for (int j = 0; j < kNi; ++j) {
-        const Quad4 qd = quad4_at<f32p>(d, n0 + xr + 16 * j + r16, 16 * (i0 + bi) + 4 * g);
-        u16x4 o;
-        quad_o(i0 + bi, j, o);
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pe = f32p ? (float)pv[bi][j][e] : bf2f((uint16_t)pv[bi][j][e]);
-          v[e] = step ? pe * wdf + bf2f(o[e]) * neg : bf2f(o[e]);
-        }
-        store_param4<f32p>(d, qd, v);
-      }
-  }
+#undef PM_SM_UNIT
+  wait_vmcnt<0>();  // no copy is still writing this block's LDS when it ends
 }
 
 }  // namespace pm
