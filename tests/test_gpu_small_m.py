@@ -194,3 +194,55 @@ def test_chunked_qkv_muon_step(ns_form, pdt):
             half_ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(got[sl]), 1e-30))) - 8)
             tol += np.linalg.norm(half_ulp) / (lr * ratio * np.linalg.norm(ref_o))
         assert rel_fro(o_got, ref_o) <= tol, k
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+def test_small_step_equals_engine_on_padded_param(ns_form, pdt):
+    """A full Muon step (MODE_STEP: momentum, NS, the fused parameter step) on
+    small matrices equals, bit for bit, the engine's step on the same matrices
+    zero-padded to a short side of 256. One call holds enough matrices that
+    each block of the streamed apply walks across several of them, ragged
+    shapes (masked edges), tall ones, and a param whose rows are not 16-byte
+    aligned (row stride 1001: the element-by-element path)."""
+    print(f"small step vs engine {ns_form} {pdt}", flush=True)
+    shapes = [(128, 1024)] * 40 + [(100, 1000), (64, 300), (2048, 128), (1000, 100), (128, 1000)]
+    params, grads, bufs, ratios = [], [], [], []
+    big = None
+    for k, (r, c) in enumerate(shapes):
+        if k == len(shapes) - 1:  # a column slice: row stride 1001 elements
+            big = seeded((r, c + 1), 400 + k, 0.02).to(pdt).to(DEV)
+            params.append(big[:, :c])
+        else:
+            params.append(seeded((r, c), 400 + k, 0.02).to(pdt).to(DEV))
+        grads.append(seeded((r, c), 500 + k, 1e-3).to(torch.bfloat16).to(DEV))
+        bufs.append(seeded((r, c), 600 + k, 1e-3).to(DEV))
+        ratios.append(muon_ref.adjust_lr_ratio("match_rms_adamw", (r, c)))
+    assert params[-1].stride(0) == 1001
+
+    def padded(t):
+        r, c = t.shape
+        if r <= c:  # wide: zero rows up to 256
+            out = torch.zeros((256, c), dtype=t.dtype, device=DEV)
+            out[:r] = t
+        else:  # tall: zero columns up to 256
+            out = torch.zeros((r, 256), dtype=t.dtype, device=DEV)
+            out[:, :c] = t
+        return out
+
+    before = [p.clone() for p in params]
+    pp = [padded(p) for p in params]
+    gp = [padded(g) for g in grads]
+    bp = [padded(b) for b in bufs]
+    kw = dict(lr=0.02, weight_decay=0.01, momentum=0.95, nesterov=True, ns_coefficients=(3.4445, -4.7750, 2.0315),
+              ns_steps=5, eps=1e-7, ns_form=ns_form)
+    _lib.muon_step(params, grads, bufs, ratios, **kw)
+    _lib.muon_step(pp, gp, bp, ratios, **kw)
+    torch.cuda.synchronize()
+    for k, (p, b, q, bq, p0) in enumerate(zip(params, bufs, pp, bp, before)):
+        r, c = p.shape
+        assert torch.equal(b, bq[:r, :c]), f"momentum of matrix {k} {r}x{c}"
+        assert torch.equal(p, q[:r, :c]), f"param of matrix {k} {r}x{c}"
+        assert not torch.equal(p, p0), f"matrix {k} {r}x{c} was not stepped"
+    # the slice's neighbouring column is untouched
+    assert torch.equal(big[:, 1000], seeded((128, 1001), 400 + len(shapes) - 1, 0.02).to(pdt).to(DEV)[:, 1000])
