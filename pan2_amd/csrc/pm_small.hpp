@@ -65,17 +65,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const uint16_t* b
   return panel_rsrc((const uint16_t*)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
 }
 
-// A 128 x 128 bf16 matrix in LDS, rows 0..63 in h[0] and 64..127 in h[1]
+// A 128 x 128 bf16 matrix in LDS, rows 0..63 in h0 and 64..127 in h1
 // (two 16 KiB gram-ring slots). Row r is 256 B and chunk c (16 B, columns
 // 8c .. 8c+7) of row r is stored at chunk c ^ (r & 15), so the 16 rows of an
 // MFMA operand read of one chunk hit 16 different bank groups. Every access
 // below names its half from wave-uniform values.
 struct SmMat {
-  char* h[2];
+  char* h0;  // rows 0..63
+  char* h1;  // rows 64..127
 };
 // chunk c16 of row (64·half + rr)
 __device__ __forceinline__ char* sm_at(const SmMat& m, int half, int rr, int c16) {
-  return m.h[half] + rr * kSmRow + ((c16 ^ (rr & 15)) << 4);
+  // a select, not h[half]: a runtime index into the pair would keep it in
+  // scratch memory and reload the base from there on every access
+  return (half ? m.h1 : m.h0) + rr * kSmRow + ((c16 ^ (rr & 15)) << 4);
 }
 // element (64·half + rr, q)
 __device__ __forceinline__ uint16_t* sm_el(const SmMat& m, int half, int rr, int q) {
@@ -272,14 +275,14 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
   ring.s[0] = g0; ring.s[1] = g1; ring.s[2] = g2; ring.s[3] = g3;
   // after the gram the ring holds the M x M matrices, two slots each
   SmMat R, Z, Q, RZ;
-  R.h[0] = g0; R.h[1] = g1; Z.h[0] = g2; Z.h[1] = g3;
+  R.h0 = g0; R.h1 = g1; Z.h0 = g2; Z.h1 = g3;
   if constexpr (RING == kSmRing) {
     __shared__ __attribute__((aligned(1024))) char g4[kSmUnit];
     __shared__ __attribute__((aligned(1024))) char g5[kSmUnit];
     __shared__ __attribute__((aligned(1024))) char g6[kSmUnit];
     __shared__ __attribute__((aligned(1024))) char g7[kSmUnit];
     ring.s[4] = g4; ring.s[5] = g5; ring.s[6] = g6; ring.s[7] = g7;
-    Q.h[0] = g4; Q.h[1] = g5; RZ.h[0] = g6; RZ.h[1] = g7;
+    Q.h0 = g4; Q.h1 = g5; RZ.h0 = g6; RZ.h1 = g7;
   }
 
   const MatDesc& d = args.descs[blockIdx.x];
@@ -333,7 +336,7 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
   sm_finish(acc, R, R, args.first ? d.scales[0] : 1.0f, 0.0f, r0, c0, lane);
 
   // ---- the M x M part of the iteration
-  const SmMat* out = &Z;
+  bool out_q = false;  // S = Z (standard form) or Q (gram form)
   if (RING == kSmRingStd || args.steps == 0) {
     const float* k = args.coeffs + 3 * args.it0;
     sm_product(R, R, R, Z, k[2], k[1], wave, lane);  // B = c R R + b R
@@ -351,14 +354,15 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
         sm_product(Z, RZ, RZ, R, 1.0f, a, wave, lane);  // R = Z RZ + a RZ
       }
     }
-    out = &Q;
+    out_q = true;
   }
 
   // ---- S (row-major 128 x 128) to the workspace
   uint16_t* S = d.S[args.so];
   for (int i = threadIdx.x; i < kSm * kSm / 8; i += blockDim.x) {
     const int r = i >> 4, c = i & 15;
-    *(u32x4*)(S + r * kSm + 8 * c) = *(const u32x4*)sm_at(*out, r >> 6, r & 63, c);
+    const SmMat out{out_q ? Q.h0 : Z.h0, out_q ? Q.h1 : Z.h1};
+    *(u32x4*)(S + r * kSm + 8 * c) = *(const u32x4*)sm_at(out, r >> 6, r & 63, c);
   }
 }
 
