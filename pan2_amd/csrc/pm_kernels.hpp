@@ -546,7 +546,7 @@ __device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArg
     sym_tile(lt, P / kTile, j.ti, j.tj);
   } else if (STAGE == ST_UPDATE) {
     // C = S·X: the large operand is the right one (Xᵀ panels, one per tile
-    // column). Measured on BASELINE config 5: UPDATE 747.6 -> 737.1 ms per
+    // column). Measured on bench.py --config 5: UPDATE 747.6 -> 737.1 ms per
     // step; a tall FINAL (the same product) measured slower this way (+2.5%)
     full_tile_cols(lt, P / kTile, Q / kTile, j.ti, j.tj);
   } else {

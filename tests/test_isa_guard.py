@@ -24,14 +24,18 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 
 @pytest.fixture(scope="module")
-def gemm_kernels(tmp_path_factory):
+def asm(tmp_path_factory):
     if not os.path.exists(HIPCC):
         pytest.skip("needs hipcc")
     out = tmp_path_factory.mktemp("isa") / "panmuon.s"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
                     "-packed-fp32-ops", "--cuda-device-only", "-S", SRC, "-o", str(out)],
                    check=True, capture_output=True)
-    asm = out.read_text()
+    return out.read_text()
+
+
+@pytest.fixture(scope="module")
+def gemm_kernels(asm):
     kernels = {}
     for m in re.finditer(r"^(_ZN2pm17pm_ns_gemm_kernel\w+):.*$", asm, flags=re.M):
         body = asm[m.end():]
@@ -84,3 +88,21 @@ def test_no_scalar_memory_writes(gemm_kernels):
     for name, lines in gemm_kernels.items():
         hits = [ln.strip() for ln in lines if bad.match(ln)]
         assert not hits, f"{name}: {hits[:2]}"
+
+
+def test_small_kernels_keep_lds_in_lds(asm):
+    """The small-matrix kernels hold their LDS addresses in registers: no
+    scratch traffic, and the core kernel's M x M products read and write LDS
+    with ds_ instructions (a pointer that went through memory turns them into
+    flat accesses that wait on both counters)."""
+    kernels = {}
+    for m in re.finditer(r"^(_ZN2pm\d+pm_small_\w+):.*$", asm, flags=re.M):
+        body = asm[m.end():]
+        kernels[m.group(1)] = body[:body.index(".Lfunc_end")]
+    assert len(kernels) == 5, sorted(kernels)
+    for name, body in kernels.items():
+        assert "scratch_" not in body, name
+        if "core_kernel" in name:
+            wide_flat = re.findall(r"^\s*flat_(load|store)_dwordx[24]", body, flags=re.M)
+            assert len(wide_flat) <= 1, f"{name}: {len(wide_flat)} flat accesses of 8 or 16 bytes"
+            assert "ds_read_b128" in body, name
