@@ -203,10 +203,12 @@ def test_small_step_equals_engine_on_padded_param(ns_form, pdt):
     small matrices equals, bit for bit, the engine's step on the same matrices
     zero-padded to a short side of 256. One call holds enough matrices that
     each block of the streamed apply walks across several of them, ragged
-    shapes (masked edges), tall ones, and a param whose rows are not 16-byte
-    aligned (row stride 1001: the element-by-element path)."""
+    shapes (masked edges; odd short sides, a single row), tall ones, and a
+    param whose rows are not 16-byte aligned (row stride 1001: the
+    element-by-element path)."""
     print(f"small step vs engine {ns_form} {pdt}", flush=True)
-    shapes = [(128, 1024)] * 40 + [(100, 1000), (64, 300), (2048, 128), (1000, 100), (128, 1000)]
+    shapes = ([(128, 1024)] * 40 + [(100, 1000), (64, 300), (2048, 128), (1000, 100), (500, 37), (37, 500), (1, 260),
+                                     (260, 3), (128, 1000)])
     params, grads, bufs, ratios = [], [], [], []
     big = None
     for k, (r, c) in enumerate(shapes):
