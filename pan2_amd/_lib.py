@@ -7,6 +7,7 @@ or fails to load, every entry point raises.
 from __future__ import annotations
 
 import ctypes
+import operator
 import os
 import threading
 
@@ -503,8 +504,15 @@ def adam_dtype_code(t: torch.Tensor) -> int:
     return code
 
 
-def _dtype_codes(ts) -> int | list[int]:
-    kinds = {t.dtype for t in ts}
+_dtype_of = operator.attrgetter("dtype")
+_data_ptr = torch.Tensor.data_ptr
+_numel = torch.Tensor.numel
+
+
+def _dtype_codes(ts, kinds=None) -> int | list[int]:
+    """One code for a list of one dtype, else one code per tensor. kinds: the
+    list's set of dtypes, when the caller has taken it already."""
+    kinds = set(map(_dtype_of, ts)) if kinds is None else kinds
     if len(kinds) == 1:
         return adam_dtype_code(ts[0])
     return [adam_dtype_code(t) for t in ts]
@@ -530,12 +538,14 @@ def _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, sta
 
 def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, *, lr, beta1: float,
               beta2: float, eps: float, weight_decay: float, amsgrad: bool, maximize: bool, decoupled: bool,
-              grad_scale=None, found_inf=None, trusted: bool = False) -> None:
+              grad_scale=None, found_inf=None, trusted: bool = False, dtype_sets=None) -> None:
     """pm_adam_step over matching lists of contiguous device tensors (updated
     in place, steps included). lr: float, or a 1-element tensor (read on the
     device when it lives there). trusted: the lists come from torch's Adam,
     whose _init_group already guarantees one device, matching shapes,
-    contiguous state and float32 device steps; only the per-call checks run."""
+    contiguous state and float32 device steps; only the per-call checks run.
+    dtype_sets: the set of dtypes of params, grads, exp_avgs and exp_avg_sqs,
+    when the caller has taken them already (the descriptors need them)."""
     lib = load()
     n = len(params)
     if n == 0:
@@ -545,21 +555,24 @@ def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps
         raise RuntimeError("pan2_amd Adam runs on HIP device tensors only; got a CPU parameter")
     if not trusted:
         _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev)
-    elif any(not g.is_contiguous() for g in grads):
+    elif not all(map(torch.Tensor.is_contiguous, grads)):
         raise ValueError("grads must be contiguous")
+    kinds = dtype_sets if dtype_sets is not None else (None,) * 4
+    # map() over the unbound methods keeps the per-tensor loop in C: this
+    # list building is most of the host time of a step over a few hundred tensors
     arr = np.zeros(n, dtype=_PM_ADAM_NP)
-    arr["param"] = [t.data_ptr() for t in params]
-    arr["grad"] = [t.data_ptr() for t in grads]
-    arr["exp_avg"] = [t.data_ptr() for t in exp_avgs]
-    arr["exp_avg_sq"] = [t.data_ptr() for t in exp_avg_sqs]
+    arr["param"] = list(map(_data_ptr, params))
+    arr["grad"] = list(map(_data_ptr, grads))
+    arr["exp_avg"] = list(map(_data_ptr, exp_avgs))
+    arr["exp_avg_sq"] = list(map(_data_ptr, exp_avg_sqs))
     if amsgrad:
-        arr["max_exp_avg_sq"] = [t.data_ptr() for t in max_exp_avg_sqs]
-    arr["step"] = [t.data_ptr() for t in state_steps]
-    arr["numel"] = [t.numel() for t in params]
-    arr["param_dtype"] = _dtype_codes(params)
-    arr["grad_dtype"] = _dtype_codes(grads)
-    arr["exp_avg_dtype"] = _dtype_codes(exp_avgs)
-    arr["exp_avg_sq_dtype"] = _dtype_codes(exp_avg_sqs)
+        arr["max_exp_avg_sq"] = list(map(_data_ptr, max_exp_avg_sqs))
+    arr["step"] = list(map(_data_ptr, state_steps))
+    arr["numel"] = list(map(_numel, params))
+    arr["param_dtype"] = _dtype_codes(params, kinds[0])
+    arr["grad_dtype"] = _dtype_codes(grads, kinds[1])
+    arr["exp_avg_dtype"] = _dtype_codes(exp_avgs, kinds[2])
+    arr["exp_avg_sq_dtype"] = _dtype_codes(exp_avg_sqs, kinds[3])
     keep = [arr]
     hp = PmAdamHparams(beta1=float(beta1), beta2=float(beta2), eps=float(eps), weight_decay=float(weight_decay),
                        amsgrad=int(bool(amsgrad)), maximize=int(bool(maximize)),

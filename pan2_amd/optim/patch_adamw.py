@@ -20,6 +20,7 @@ unpatched process would run them; fp32, bf16 and fp16 device tensors go to
 from __future__ import annotations
 
 import importlib
+import operator
 
 import torch
 from torch import Tensor
@@ -30,6 +31,9 @@ from .. import _lib
 _adam_module = importlib.import_module("torch.optim.adam")
 # torch's own fused Adam, for the tensors pm_adam_step does not take
 _torch_fused_adam = _adam_module._fused_adam
+
+_get_device = Tensor.get_device
+_dtype_of = operator.attrgetter("dtype")
 
 
 def _scalar(x):
@@ -71,6 +75,27 @@ def _fused_adam(
         return
     if differentiable:
         raise RuntimeError("Adam with fused=True does not support differentiable=True")
+    beta1, beta2 = _scalar(beta1), _scalar(beta2)
+    # The common case, scanned list by list: every tensor on one HIP device
+    # (get_device is -1 on the CPU) with a dtype pm_adam_step takes.
+    lists = (params, grads, exp_avgs, exp_avg_sqs) + ((max_exp_avg_sqs,) if amsgrad else ())
+    devs = [set(map(_get_device, xs)) for xs in lists]
+    kinds = [set(map(_dtype_of, xs)) for xs in lists]
+    if (params[0].is_cuda and len(devs[0]) == 1 and all(d == devs[0] for d in devs)
+            and all(k <= _lib.ADAM_DTYPES.keys() for k in kinds)):
+        dev = params[0].device
+        dev_lr = lr
+        if isinstance(lr, Tensor) and lr.device.type != "cpu" and lr.device != dev:
+            dev_lr = lr.to(device=dev, non_blocking=True)
+        _lib.adam_step(
+            params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs if amsgrad else [None] * len(params), state_steps,
+            lr=dev_lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+            maximize=maximize, decoupled=decoupled_weight_decay,
+            grad_scale=None if grad_scale is None else grad_scale.to(dev, non_blocking=True),
+            found_inf=None if found_inf is None else found_inf.to(dev, non_blocking=True),
+            trusted=True, dtype_sets=kinds[:4],
+        )
+        return
     mine = [_native(i, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, amsgrad) for i in range(len(params))]
     if not all(mine):
         rest = [i for i, m in enumerate(mine) if not m]
@@ -86,7 +111,6 @@ def _fused_adam(
         pick = lambda xs: [xs[i] for i in keep] if xs else xs  # noqa: E731
         params, grads, exp_avgs, exp_avg_sqs = pick(params), pick(grads), pick(exp_avgs), pick(exp_avg_sqs)
         max_exp_avg_sqs, state_steps = pick(max_exp_avg_sqs), pick(state_steps)
-    beta1, beta2 = _scalar(beta1), _scalar(beta2)
     by_device: dict[torch.device, list[int]] = {}
     for i, p in enumerate(params):
         by_device.setdefault(p.device, []).append(i)

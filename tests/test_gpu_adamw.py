@@ -153,16 +153,17 @@ def _torch_vs_ours(torch_fused_adam, *, lr, grad_scale=None, found_inf=None, pdt
     from pan2_amd.optim import patch_adamw
 
     sizes = [8193, 100003, 5, 4096]
+    pdts = list(pdt) if isinstance(pdt, (list, tuple)) else [pdt] * len(sizes)
     results = []
     for ours in (False, True):
-        ps = [torch.from_numpy(rnd(n, 50 + i, 0.5)).to(DEV, pdt) for i, n in enumerate(sizes)]
+        ps = [torch.from_numpy(rnd(n, 50 + i, 0.5)).to(DEV, pdts[i]) for i, n in enumerate(sizes)]
         ms = [torch.zeros_like(p) for p in ps]
         vs = [torch.zeros_like(p) for p in ps]
         xs = [torch.zeros_like(p) for p in ps] if amsgrad else []
         st = [torch.zeros((), dtype=torch.float32, device=DEV) for _ in ps]
         gs_all = []
         for k in range(steps):
-            gs = [torch.from_numpy(rnd(n, 70 + 10 * k + i, gscale)).to(DEV, pdt) for i, n in enumerate(sizes)]
+            gs = [torch.from_numpy(rnd(n, 70 + 10 * k + i, gscale)).to(DEV, pdts[i]) for i, n in enumerate(sizes)]
             kw = dict(amsgrad=amsgrad, has_complex=False, beta1=0.95, beta2=0.95, lr=lr, weight_decay=wd, eps=1e-8,
                       maximize=False, capturable=False, differentiable=False, decoupled_weight_decay=decoupled)
             if ours:
@@ -201,6 +202,19 @@ def test_matches_torch_fused_adam_amsgrad_and_bf16(torch_fused_adam):
         # bf16 storage: one bf16 rounding of values that agree to a few fp32 ulps
         for a, b in ((m[i], tm[i]), (v[i], tv[i]), (x[i], tx[i]), (p[i], tp[i])):
             assert np.all(np.abs(a - b) <= ulp(b, "bf16") + 1e-6 * np.abs(b).max())
+
+
+def test_mixed_dtype_lists_match_torch_fused_adam(torch_fused_adam):
+    """One call whose lists mix fp32, bf16 and fp16 tensors (each with state of
+    its param's dtype): torch's fused Adam splits them by dtype, the patched one
+    takes them in one launch with a dtype code per tensor."""
+    pdts = [torch.float32, torch.bfloat16, torch.float16, torch.float32]
+    (tp, tm, tv, _, tst, _), (p, m, v, _, st, _) = _torch_vs_ours(torch_fused_adam, lr=1e-3, pdt=pdts, gscale=1.0)
+    assert st == tst
+    for i, dt in enumerate(("f32", "bf16", "f16", "f32")):
+        for a, b in ((m[i], tm[i]), (v[i], tv[i]), (p[i], tp[i])):
+            tol = 2e-6 * np.abs(b) if dt == "f32" else ulp(b, dt)
+            assert np.all(np.abs(a - b) <= tol + 1e-6 * np.abs(b).max()), (i, dt)
 
 
 def test_matches_torch_fused_adam_fp16(torch_fused_adam):
