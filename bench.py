@@ -216,8 +216,10 @@ def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
 
 def probe_ceiling(units: int = 3000) -> int:
     """MFMA ceilings of the GEMM engine's loop on this chip (pan2_amd/csrc/pm_probe.hip):
-    MFMA alone, MFMA with the engine's LDS fragment reads and barriers, and the
-    same with 4 waves of 128 x 128; one line each."""
+    MFMA alone; with the engine's LDS fragment reads and barriers (8 waves of
+    128 x 64, then 4 waves of 128 x 128); and the 8-wave loop with the engine's
+    global -> LDS copies, from a 64 MiB window per XCD and from one 1 MiB window
+    that stays in L2. One line each, two rounds."""
     import ctypes
 
     import torch
@@ -229,23 +231,29 @@ def probe_ceiling(units: int = 3000) -> int:
     lib = ctypes.CDLL(PROBE_LIB)
     fn = lib.pp_ceiling
     fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
-                   ctypes.POINTER(ctypes.c_double)]
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint,
+                   ctypes.c_int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_double)]
     out = torch.empty(cus * 512, dtype=torch.float32, device=dev)
-    names = {0: "mfma only (8 waves of 128x64 accumulators, register operands)",
-             1: "mfma + LDS fragment reads + 2 barriers per 64-deep unit (8 waves of 128x64)",
-             2: "mfma + LDS fragment reads + 2 barriers per 64-deep unit (4 waves of 128x128)"}
-    for which in (0, 1, 2, 0, 1, 2):
-        ms, fl = ctypes.c_float(), ctypes.c_double()
-        torch.cuda.synchronize()
-        rc = fn(which, cus, units if which != 2 else units // 2, ctypes.c_void_p(out.data_ptr()), ctypes.byref(ms),
-                ctypes.byref(fl))
-        if rc != 0:
-            print(f"probe ceiling {which}: failed", file=sys.stderr)
-            return 1
-        tf = fl.value / (ms.value * 1e-3) / 1e12
-        print(f"probe ceiling {which}: {tf:.1f} TFLOP/s = {100 * tf / PEAK_BF16_TFLOPS:.1f}% of {PEAK_BF16_TFLOPS} "
-              f"({ms.value:.3f} ms) -- {names[which]}", flush=True)
+    mib = 1 << 20
+    src = torch.empty(8 * 64 * mib // 2, dtype=torch.int16, device=dev)
+    src.random_(0, 1 << 14).bitwise_or_(0x3c00)  # bf16 in [2^-7, 2) with random mantissas, as the LDS data
+    cases = [(0, 0, 1, "mfma only (8 waves of 128x64 accumulators, register operands)"),
+             (1, 0, 1, "mfma + LDS fragment reads + 2 barriers per 64-deep unit (8 waves of 128x64)"),
+             (2, 0, 1, "mfma + LDS fragment reads + 2 barriers per 64-deep unit (4 waves of 128x128)"),
+             (3, 64 * mib, 8, "as 1 + the engine's global->LDS copies, a 64 MiB window per XCD"),
+             (3, 1 * mib, 1, "as 1 + the engine's global->LDS copies, one 1 MiB window (L2-resident)")]
+    for _ in range(2):
+        for which, span, nwin, name in cases:
+            ms, fl = ctypes.c_float(), ctypes.c_double()
+            torch.cuda.synchronize()
+            rc = fn(which, cus, units if which != 2 else units // 2, ctypes.c_void_p(out.data_ptr()),
+                    ctypes.c_void_p(src.data_ptr()), span, nwin, ctypes.byref(ms), ctypes.byref(fl))
+            if rc != 0:
+                print(f"probe ceiling {which}: failed", file=sys.stderr)
+                return 1
+            tf = fl.value / (ms.value * 1e-3) / 1e12
+            print(f"probe ceiling {which}: {tf:.1f} TFLOP/s = {100 * tf / PEAK_BF16_TFLOPS:.1f}% of "
+                  f"{PEAK_BF16_TFLOPS} ({ms.value:.3f} ms) -- {name}", flush=True)
     return 0
 
 
