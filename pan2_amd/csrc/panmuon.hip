@@ -362,32 +362,36 @@ struct Launcher {
     timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
     return check("Newton-Schulz update launch");
   }
-  // small matrices: R = X Xᵀ and the M x M part of `steps` iterations from it0
-  // (steps == 0: the standard form's B) into S[0]
+  // small matrices: R = X Xᵀ (or, r_in, the R an apply left in S[0]) and the
+  // M x M part of `steps` iterations from it0 (steps == 0: the standard form's
+  // B) into S[0]
   const float* coeffs = nullptr;  // device (a, b, c) per iteration
-  int small_core(int cur, bool first, int it0, int steps, int it) {
-    const SmallCoreArgs a{ga.descs, coeffs, it0, steps, cur, first, 0, 0};
+  int small_core(int cur, bool first, int it0, int steps, int it, bool r_in = false) {
+    const SmallCoreArgs a{ga.descs, coeffs, it0, steps, cur, first, 0, r_in};
     if (steps == 0)  // the standard form's M x M part fits a 4-slot ring: two blocks per CU
       hipLaunchKernelGGL(pm_small_core_kernel<kSmRingStd>, dim3(count), dim3(kGemmThreads), 0, stream, a);
     else
       hipLaunchKernelGGL(pm_small_core_kernel<kSmRing>, dim3(count), dim3(kGemmThreads), 0, stream, a);
     const int products = steps == 0 ? 1 : 4 * steps - 3;
-    timing_mark(stream, PM_K_SMALL_CORE, group, it, count, f_gram + products * f_sym, 0.0);
+    timing_mark(stream, PM_K_SMALL_CORE, group, it, count, (r_in ? 0.0 : f_gram) + products * f_sym, 0.0);
     return check("small-matrix core launch");
   }
-  // small matrices: X' = s·(a·X + S[0]·X), or (last) the param step
-  int small_apply(float coef_a, int cur, bool first, bool last, int it) {
+  // small matrices: X' = s·(a·X + S[0]·X), or (last) the param step; gram:
+  // also R = X' X'ᵀ into S[0] for the next core launch (r_in)
+  int small_apply(float coef_a, int cur, bool first, bool last, int it, bool gram = false) {
     GemmArgs a = ga;
-    a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = 0; a.a = coef_a; a.cur = cur; a.first = first;
+    a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = 0; a.sc = 0; a.a = coef_a; a.cur = cur; a.first = first;
     a.prefix = full; a.total = full_total;
     const dim3 grid(full_grid), block(kSmApplyThreads);  // persistent: one block per CU
     if (last && final_f32)
       hipLaunchKernelGGL((pm_small_apply_kernel<ST_FINAL, DT_F32>), grid, block, 0, stream, a);
     else if (last)
       hipLaunchKernelGGL((pm_small_apply_kernel<ST_FINAL, DT_BF16>), grid, block, 0, stream, a);
+    else if (gram)
+      hipLaunchKernelGGL((pm_small_apply_kernel<ST_UPDATE, DT_BF16, true>), grid, block, 0, stream, a);
     else
       hipLaunchKernelGGL((pm_small_apply_kernel<ST_UPDATE, DT_BF16>), grid, block, 0, stream, a);
-    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
+    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd + (gram ? f_gram : 0.0), 0.0);
     return check("small-matrix apply launch");
   }
   int qinit(int sz, int sq, float coef_a, int max_mp, int it) {
@@ -473,13 +477,19 @@ int run_gram(Launcher& L, const pm_hparams* hp, int max_mp) {
 // (R and B) and one apply. Gram form: one core launch per segment (R, then the
 // segment's Z, Q and R updates) and one apply of its Q, the second segment
 // starting at the reset iteration on the applied X.
-int run_small(Launcher& L, const pm_hparams* hp) {
+// When the group has many matrices (fused), an apply that is followed by a
+// core launch also forms that launch's R from the X' it writes, so the core
+// launch reads R (32 KiB a matrix) instead of X' (256 B per column). The fused
+// apply gives each block whole matrices, so a group of few long matrices keeps
+// the separate gram, which spreads one matrix over many blocks.
+int run_small(Launcher& L, const pm_hparams* hp, bool fused) {
   const int steps = hp->ns_steps;
   if (hp->ns_form != NS_GRAM) {
     const Coeffs co{hp};
     for (int it = 0; it < steps; ++it) {
-      int rc = L.small_core(it & 1, it == 0, it, 0, it);
-      if (!rc) rc = L.small_apply(co.at(it).a, it & 1, it == 0, it + 1 == steps, it);
+      const bool r_in = fused && it > 0, last = it + 1 == steps;
+      int rc = L.small_core(it & 1, it == 0, it, 0, it, r_in);
+      if (!rc) rc = L.small_apply(co.at(it).a, it & 1, it == 0, last, it, fused && !last);
       if (rc) return rc;
     }
     return PM_OK;
@@ -487,9 +497,9 @@ int run_small(Launcher& L, const pm_hparams* hp) {
   const int reset = gram_reset(steps);
   const int seg1 = reset > 0 ? reset : steps;
   int rc = L.small_core(0, true, 0, seg1, 0);
-  if (!rc) rc = L.small_apply(0.0f, 0, true, seg1 == steps, seg1 - 1);
+  if (!rc) rc = L.small_apply(0.0f, 0, true, seg1 == steps, seg1 - 1, fused && seg1 < steps);
   if (!rc && seg1 < steps) {
-    rc = L.small_core(1, false, seg1, steps - seg1, seg1);
+    rc = L.small_core(1, false, seg1, steps - seg1, seg1, fused);
     if (!rc) rc = L.small_apply(0.0f, 1, false, true, steps - 1);
   }
   return rc;
@@ -622,7 +632,14 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   L.f_sym = f_sym;
   L.f_upd = f_upd;
   L.coeffs = (const float*)(ws + ((char*)coeffs - host.data()));
-  if (items[0].plan.small) return run_small(L, hp);
+  if (items[0].plan.small) {
+    // fused gram: at least one matrix per apply block, none longer than
+    // twice a block's even share of the units
+    int32_t longest = 0;
+    for (int i = 0; i < count; ++i) longest = std::max(longest, full[i + 1] - full[i]);
+    const bool fused = count >= L.full_grid && (int64_t)longest * L.full_grid <= 2 * (int64_t)full[count];
+    return run_small(L, hp, fused);
+  }
   return form == NS_GRAM ? run_gram(L, hp, max_mp) : run_standard(L, hp);
 }
 

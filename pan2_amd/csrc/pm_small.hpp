@@ -50,7 +50,7 @@ struct SmallCoreArgs {
   int32_t cur;          // X slot holding the current X
   int32_t first;        // scale R by 1/‖X‖² (the Frobenius normalisation, folded)
   int32_t so;           // square buffer receiving S
-  int32_t pad_;
+  int32_t r_in;         // R is already in S[so] (written by the apply that made X): skip the gram
 };
 
 // A buffer resource over [base, base + bytes). Descriptor fields reach
@@ -84,6 +84,18 @@ __device__ __forceinline__ char* sm_at(const SmMat& m, int half, int rr, int c16
 __device__ __forceinline__ uint16_t* sm_el(const SmMat& m, int half, int rr, int q) {
   return (uint16_t*)(sm_at(m, half, rr, q >> 3) + (q & 7) * 2);
 }
+
+// 16-byte LDS accesses through a pointer the compiler may only know as
+// generic (an LDS matrix picked at run time): the cast keeps them ds_
+// instructions rather than flat ones, which would also count in vmcnt.
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+__device__ __forceinline__ u32x4 lds_load16(const char* p) { return *(const lds_u32x4*)(p); }
+__device__ __forceinline__ void lds_store16(char* p, u32x4 v) { *(lds_u32x4*)(p) = v; }
+// and 16-byte accesses of the workspace, whose pointers come from the
+// descriptor table (global_ rather than flat instructions)
+typedef __attribute__((address_space(1))) u32x4 glb_u32x4;
+__device__ __forceinline__ u32x4 glb_load16(const uint16_t* p) { return *(const glb_u32x4*)(p); }
+__device__ __forceinline__ void glb_store16(uint16_t* p, u32x4 v) { *(glb_u32x4*)(p) = v; }
 
 __device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -230,18 +242,11 @@ struct SmCopy {
   }
 };
 
-// One unit in slot S of a ring of RING slots: wait for it, refill the slot read
-// last (unit u-1's) with unit u + RING - 1, accumulate the unit's two k-steps.
-// The barrier is a bare s_barrier: __syncthreads' fence would drain every copy
-// in flight.
-template <int RING, int S>
-__device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy, int u, int KT, f32x4 (&acc)[4][2],
-                                          int r0, int c0, int lane) {
-  wait_units(min(RING - 2, KT - 1 - u));  // this wave's copies of unit u have landed
-  block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
-  if (u + RING - 1 < KT) copy(ring.s[(S + RING - 1) % RING], u + RING - 1);
+// The gram's two k-steps over one unit in LDS (rows 0..127 of 64 k values,
+// chunk c of row r stored at chunk c ^ ((r >> 1) & 7)): wave w accumulates rows
+// r0 .. r0+63 of columns c0 .. c0+31 of R = X Xᵀ (the layout sm_finish takes).
+__device__ __forceinline__ void sm_gram_acc(const char* src, f32x4 (&acc)[4][2], int r0, int c0, int lane) {
   if (sm_idle(r0, c0)) return;
-  const char* src = ring.s[S];
   const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
@@ -256,6 +261,60 @@ __device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
   }
+}
+
+// R = bf16(acc) written row-major (128 x 128) to global memory, through the
+// LDS matrix T: elements on and above the diagonal at (p, q) and (q, p), as
+// sm_finish writes them with alpha = 1, beta = 0 (the same expression, so the
+// same bits), then whole rows out with 16-byte stores. Every wave of the block
+// calls it: it begins with a barrier (every wave's earlier reads of T's tiles
+// have completed: their MFMAs consumed them) and ends with one (every read of T
+// is done, so the tiles may be written again). The barriers are bare: a
+// __syncthreads fence would also wait for the copies in flight.
+__device__ __forceinline__ void sm_gram_store(uint16_t* Rg, const SmMat& T, const f32x4 (&acc)[4][2], int r0, int c0,
+                                              int lane) {
+#pragma clang fp contract(off)
+  const int g = lane >> 4;
+  const int rh = r0 >> 6, ch = c0 >> 6, cr = c0 & 63;
+  const float alpha = 1.0f, beta = 0.0f;
+  u16x4 o[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[i][j][r] = f2bf(alpha * acc[i][j][r] + beta * bf2f((uint16_t)0));
+  block_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int p0 = r0 + 16 * i + 4 * g, q = c0 + 16 * j + (lane & 15);
+      store_upper4(sm_el(T, rh, 16 * i + 4 * g + (lane & 3), q & ~3), quad_transpose(o[i][j], lane), q & ~3,
+                   p0 + (lane & 3));
+      store_lower4(sm_el(T, ch, cr + 16 * j + (lane & 15), p0), o[i][j], p0, q);
+    }
+  wait_lgkmcnt<0>();
+  block_barrier();
+  for (int i = threadIdx.x; i < kSm * kSm / 8; i += blockDim.x) {
+    const int r = i >> 4, c = i & 15;
+    glb_store16(Rg + r * kSm + 8 * c, lds_load16(sm_at(T, r >> 6, r & 63, c)));
+  }
+  wait_lgkmcnt<0>();
+  block_barrier();
+}
+
+// One unit in slot S of a ring of RING slots: wait for it, refill the slot read
+// last (unit u-1's) with unit u + RING - 1, accumulate the unit's two k-steps.
+// The barrier is a bare s_barrier: __syncthreads' fence would drain every copy
+// in flight.
+template <int RING, int S>
+__device__ __forceinline__ void gram_unit(const SmRing& ring, const SmCopy& copy, int u, int KT, f32x4 (&acc)[4][2],
+                                          int r0, int c0, int lane) {
+  wait_units(min(RING - 2, KT - 1 - u));  // this wave's copies of unit u have landed
+  block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
+  if (u + RING - 1 < KT) copy(ring.s[(S + RING - 1) % RING], u + RING - 1);
+  sm_gram_acc(ring.s[S], acc, r0, c0, lane);
 }
 
 // One block of 8 waves per small matrix of the group (grid = matrices).
@@ -289,51 +348,61 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
   const int wave = wave_id(), lane = lane_id();
   const int r0 = (wave >> 2) * 64, c0 = (wave & 3) * 32;
 
-  // ---- R = X Xᵀ over k < Np
-  const int K = __builtin_amdgcn_readfirstlane(d.Np), KT = K / 64;
-  SmCopy copy;
-  copy.rsrc = uniform_rsrc(d.X[args.cur], (uint32_t)kSm * K * 2);
-  copy.wave = wave;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {  // copy q = 2w + h: row 8q + lane/8, stored chunk lane%8
-    const int q = 2 * wave + h;
-    const int sw = (4 * (q & 1) + (lane >> 4)) & 7;  // ((8q + lane/8) >> 1) & 7
-    copy.voff[h] = (lane >> 3) * 128 + (((lane & 7) ^ sw) << 4);
-  }
-  f32x4 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < RING - 1; ++i)
-    if (i < KT) copy(ring.s[i], i);
-  int u = 0;
-  for (; u + RING <= KT; u += RING) {
-    gram_unit<RING, 0>(ring, copy, u, KT, acc, r0, c0, lane);
-    gram_unit<RING, 1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
-    gram_unit<RING, 2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
-    gram_unit<RING, 3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
-    if constexpr (RING == kSmRing) {
-      gram_unit<RING, 4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
-      gram_unit<RING, 5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
-      gram_unit<RING, 6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
-      gram_unit<RING, 7>(ring, copy, u + 7, KT, acc, r0, c0, lane);
+  if (args.r_in) {
+    // ---- R from S[so], where the apply that produced X stored it
+    const uint16_t* Rg = d.S[args.so];
+    for (int i = threadIdx.x; i < kSm * kSm / 8; i += blockDim.x) {
+      const int r = i >> 4, c = i & 15;
+      lds_store16(sm_at(R, r >> 6, r & 63, c), glb_load16(Rg + r * kSm + 8 * c));
     }
+    __syncthreads();
+  } else {
+    // ---- R = X Xᵀ over k < Np
+    const int K = __builtin_amdgcn_readfirstlane(d.Np), KT = K / 64;
+    SmCopy copy;
+    copy.rsrc = uniform_rsrc(d.X[args.cur], (uint32_t)kSm * K * 2);
+    copy.wave = wave;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // copy q = 2w + h: row 8q + lane/8, stored chunk lane%8
+      const int q = 2 * wave + h;
+      const int sw = (4 * (q & 1) + (lane >> 4)) & 7;  // ((8q + lane/8) >> 1) & 7
+      copy.voff[h] = (lane >> 3) * 128 + (((lane & 7) ^ sw) << 4);
+    }
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < RING - 1; ++i)
+      if (i < KT) copy(ring.s[i], i);
+    int u = 0;
+    for (; u + RING <= KT; u += RING) {
+      gram_unit<RING, 0>(ring, copy, u, KT, acc, r0, c0, lane);
+      gram_unit<RING, 1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
+      gram_unit<RING, 2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
+      gram_unit<RING, 3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
+      if constexpr (RING == kSmRing) {
+        gram_unit<RING, 4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
+        gram_unit<RING, 5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
+        gram_unit<RING, 6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
+        gram_unit<RING, 7>(ring, copy, u + 7, KT, acc, r0, c0, lane);
+      }
+    }
+    if (u < KT) gram_unit<RING, 0>(ring, copy, u, KT, acc, r0, c0, lane);
+    if (u + 1 < KT) gram_unit<RING, 1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
+    if (u + 2 < KT) gram_unit<RING, 2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
+    if constexpr (RING == kSmRing) {
+      if (u + 3 < KT) gram_unit<RING, 3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
+      if (u + 4 < KT) gram_unit<RING, 4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
+      if (u + 5 < KT) gram_unit<RING, 5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
+      if (u + 6 < KT) gram_unit<RING, 6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
+    }
+    // R = s²·X Xᵀ (s² = 1/‖X‖² on the unscaled first X): sm_finish's first
+    // barrier also ends every wave's reads of the ring, whose first two slots
+    // R overwrites (every copy has landed: the last unit waited for all)
+    sm_finish(acc, R, R, args.first ? d.scales[0] : 1.0f, 0.0f, r0, c0, lane);
   }
-  if (u < KT) gram_unit<RING, 0>(ring, copy, u, KT, acc, r0, c0, lane);
-  if (u + 1 < KT) gram_unit<RING, 1>(ring, copy, u + 1, KT, acc, r0, c0, lane);
-  if (u + 2 < KT) gram_unit<RING, 2>(ring, copy, u + 2, KT, acc, r0, c0, lane);
-  if constexpr (RING == kSmRing) {
-    if (u + 3 < KT) gram_unit<RING, 3>(ring, copy, u + 3, KT, acc, r0, c0, lane);
-    if (u + 4 < KT) gram_unit<RING, 4>(ring, copy, u + 4, KT, acc, r0, c0, lane);
-    if (u + 5 < KT) gram_unit<RING, 5>(ring, copy, u + 5, KT, acc, r0, c0, lane);
-    if (u + 6 < KT) gram_unit<RING, 6>(ring, copy, u + 6, KT, acc, r0, c0, lane);
-  }
-  // R = s²·X Xᵀ (s² = 1/‖X‖² on the unscaled first X): sm_finish's first
-  // barrier also ends every wave's reads of the ring, whose first two slots
-  // R overwrites (every copy has landed: the last unit waited for all)
-  sm_finish(acc, R, R, args.first ? d.scales[0] : 1.0f, 0.0f, r0, c0, lane);
 
   // ---- the M x M part of the iteration
   bool out_q = false;  // S = Z (standard form) or Q (gram form)
@@ -362,7 +431,7 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
   for (int i = threadIdx.x; i < kSm * kSm / 8; i += blockDim.x) {
     const int r = i >> 4, c = i & 15;
     const SmMat out{out_q ? Q.h0 : Z.h0, out_q ? Q.h1 : Z.h1};
-    *(u32x4*)(S + r * kSm + 8 * c) = *(const u32x4*)sm_at(out, r >> 6, r & 63, c);
+    glb_store16(S + r * kSm + 8 * c, lds_load16(sm_at(out, r >> 6, r & 63, c)));
   }
 }
 
@@ -435,6 +504,15 @@ __device__ __forceinline__ void store_param4(const MatDesc& d, const Quad4& q, c
 // The products are the grouped engine's UPDATE / FINAL element for element
 // (the same MFMA over the same k order, bf16 rounding at the same points, the
 // same fp32 step), so the result equals the engine's on the zero-padded matrix.
+//
+// GRAM (UPDATE only): the apply also forms the next iteration's R = X' X'ᵀ,
+// which the core kernel would otherwise compute by reading X' back. Each unit's
+// X' goes to an LDS tile in the gram ring's layout, and after the next unit's
+// barrier every wave adds its two k-steps to the core's accumulators (the same
+// MFMAs in the same order, so the same R). Blocks then take whole matrices
+// (the gram of one matrix is one chain), and R is written to S[sc] when the
+// walk leaves the matrix: S, read into registers on entry, is no longer needed
+// by anyone.
 template <int STAGE, int PDT>
 struct SmApply {
   static constexpr bool kFinal = STAGE == ST_FINAL;
@@ -451,7 +529,7 @@ struct SmApply {
   // (copies are issued right after each unit's barrier, its stores last)
   static constexpr int kWaitMax = (kRing - 2) * kCopies + (kRing - 1) * kStores;
   static_assert(kWaitMax < 64, "vmcnt range");
-  static_assert(kRing * (kSmUnit + (kFinal ? kPBytes : 0)) <= 160 * 1024, "LDS");
+  static_assert((kRing + (kFinal ? 0 : 2)) * kSmUnit + (kFinal ? kRing * kPBytes : 0) <= 160 * 1024, "LDS");
 };
 
 // Waits for the copies of the r-th unit of a block (r counted from 0).
@@ -505,9 +583,10 @@ __device__ __forceinline__ int pb_off(int r, int byte) {
   return r * RB + ((((byte >> 4) ^ (r & kSwz))) << 4) + (byte & 15);
 }
 
-template <int STAGE, int PDT>
+template <int STAGE, int PDT, bool GRAM = false>
 __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(GemmArgs args) {
 #pragma clang fp contract(off)
+  static_assert(!GRAM || STAGE == ST_UPDATE, "the gram of X' is formed by the UPDATE apply");
   typedef SmApply<STAGE, PDT> C;
   constexpr bool kFinal = C::kFinal, kF32 = C::kF32;
   constexpr int kRing = C::kRing, kEsz = C::kEsz;
@@ -531,6 +610,14 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
     __shared__ __attribute__((aligned(1024))) char x7[kSmUnit];
     sl.x[4] = x4; sl.x[5] = x5; sl.x[6] = x6; sl.x[7] = x7;
   }
+  char* gt0 = nullptr;  // GRAM: X' of even / odd units, in the gram ring's layout
+  char* gt1 = nullptr;
+  if constexpr (GRAM) {
+    __shared__ __attribute__((aligned(1024))) char gx0[kSmUnit];
+    __shared__ __attribute__((aligned(1024))) char gx1[kSmUnit];
+    gt0 = gx0;
+    gt1 = gx1;
+  }
   if constexpr (kFinal) {
     __shared__ __attribute__((aligned(1024))) char p0[C::kPBytes];
     __shared__ __attribute__((aligned(1024))) char p1[C::kPBytes];
@@ -544,8 +631,17 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
 
   const SmDescPtr descs = (SmDescPtr)args.descs;
   const SmPrefixPtr prefix = (SmPrefixPtr)args.prefix;
-  const int u0 = (int)((int64_t)blockIdx.x * args.total / gridDim.x);
-  const int u1 = (int)((int64_t)(blockIdx.x + 1) * args.total / gridDim.x);
+  int u0 = (int)((int64_t)blockIdx.x * args.total / gridDim.x);
+  int u1 = (int)((int64_t)(blockIdx.x + 1) * args.total / gridDim.x);
+  if constexpr (GRAM) {
+    // whole matrices: the first matrix starting at or after each even split
+    auto bound = [&](int u) {
+      const int m = find_matrix(prefix, args.n, u);
+      return prefix[m] < u ? prefix[m + 1] : prefix[m];
+    };
+    u0 = bound(u0);
+    u1 = bound(u1);
+  }
   if (u0 >= u1) return;
   const int w = wave_id(), lane = lane_id();
   const int r16 = lane & 15, g = lane >> 4;
@@ -638,6 +734,32 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
   };
   const float wdf = step ? (args.lr_dev ? 1.0f - lr * args.wd : args.wdf_host) : 0.0f;
 
+  // GRAM: this wave's part of R (the core's layout), the unit whose X' waits
+  // in its LDS tile, and the matrix whose last unit that is (-1: none)
+  f32x4 gacc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) gacc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int gr0 = (w >> 2) * 64, gc0 = (w & 3) * 32;
+  bool gpend = false;
+  int gfin = -1;
+  // adds the waiting unit (in tile gt) to R and, at a matrix's end, writes R
+  // to its S[sc]
+  auto gram_catch_up = [&](const char* gt) {
+    if (!gpend) return;
+    sm_gram_acc(gt, gacc, gr0, gc0, lane);
+    if (gfin >= 0) {
+      sm_gram_store(descs[gfin].S[args.sc], SmMat{gt0, gt1}, gacc, gr0, gc0, lane);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) gacc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      gfin = -1;
+    }
+    gpend = false;
+  };
+
   // prologue: the first kRing - 1 units
 #pragma unroll
   for (int s = 0; s < kRing - 1; ++s) issue(sl.x[s], sl.p[s & 3]);
@@ -645,9 +767,18 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
 
   // one unit in slot S: wait for its copies, release slot S-1 to the copy
   // walk, multiply, store
-  auto unit = [&](char* xs, const char* ps, char* nxs, char* nps, int u) {
+  // GRAM: gt receives this unit's X', gp holds unit u-1's. Both are named by
+  // the ring slot (kRing is even, so consecutive units alternate tiles), which
+  // lets the compiler see that they are not the copies' targets; through a
+  // pointer chosen at run time it would wait for every copy in flight before
+  // touching them.
+  auto unit = [&](char* xs, const char* ps, char* nxs, char* nps, int u, char* gt, const char* gp) {
     wait_unit<C>(u - u0);
+    if constexpr (GRAM) wait_lgkmcnt<0>();  // this wave's X' tile writes of unit u-1 are done
     block_barrier();  // every wave's copies of u have landed; every wave is done with unit u-1
+    // unit u-1's X' is in its tile (written before the barrier); its gram, and
+    // R of a finished matrix, before this unit's copies
+    if constexpr (GRAM) gram_catch_up(gp);
     if (kw.lu == kw.nu) {  // the walk enters the next matrix
       ++kw.m;
       kw.lu = 0;
@@ -720,7 +851,14 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int pr = 64 * wr + 16 * i + 4 * g + (lane & 3), q4 = (16 * wc + r16) & ~3;
-        *(u16x4*)(xn + pr * 64 + q4) = quad_transpose(o[i], lane);
+        const u16x4 t = quad_transpose(o[i], lane);
+        *(u16x4*)(xn + pr * 64 + q4) = t;
+        // GRAM: row pr, columns q4 .. q4+3 of the unit, chunk q4/8 stored at (q4/8) ^ ((pr >> 1) & 7)
+        if constexpr (GRAM) *(u16x4*)(gt + pr * 128 + ((((q4 >> 3) ^ ((pr >> 1) & 7))) << 4) + (q4 & 7) * 2) = t;
+      }
+      if constexpr (GRAM) {
+        gpend = true;
+        if (kw.lu == kw.nu) gfin = kw.m;
       }
       return;
     }
@@ -787,8 +925,10 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
   };
 
   // slot S holds unit u0 + S (mod kRing); unit S releases slot S - 1 to the copy walk
+  static_assert(!GRAM || kRing % 2 == 0, "X' tiles alternate with the ring slots");
 #define PM_SM_UNIT(S)                                                                                 \
-  unit(sl.x[S], sl.p[(S) & 3], sl.x[((S) + kRing - 1) % kRing], sl.p[(((S) + kRing - 1) % kRing) & 3], u + (S))
+  unit(sl.x[S], sl.p[(S) & 3], sl.x[((S) + kRing - 1) % kRing], sl.p[(((S) + kRing - 1) % kRing) & 3], u + (S), \
+       ((S) & 1) ? gt1 : gt0, ((S) & 1) ? gt0 : gt1)
   for (int u = u0; u < u1; u += kRing) {
     PM_SM_UNIT(0);
     if (u + 1 >= u1) break;
@@ -811,6 +951,11 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
     }
   }
 #undef PM_SM_UNIT
+  if constexpr (GRAM) {
+    wait_lgkmcnt<0>();
+    block_barrier();  // every wave's X' of the block's last unit is in its tile
+    gram_catch_up(((u1 - 1 - u0) & 1) ? gt1 : gt0);
+  }
   wait_vmcnt<0>();  // no copy is still writing this block's LDS when it ends
 }
 

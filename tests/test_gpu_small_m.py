@@ -248,3 +248,71 @@ def test_small_step_equals_engine_on_padded_param(ns_form, pdt):
         assert not torch.equal(p, p0), f"matrix {k} {r}x{c} was not stepped"
     # the slice's neighbouring column is untouched
     assert torch.equal(big[:, 1000], seeded((128, 1001), 400 + len(shapes) - 1, 0.02).to(pdt).to(DEV)[:, 1000])
+
+
+def _many_small_shapes(n, seed):
+    """n small matrices of random short side 1..128 and long side 60..700, wide and tall."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for _ in range(n):
+        m, k = int(rng.integers(1, 129)), int(rng.integers(60, 701))
+        shapes.append((m, k) if rng.integers(2) else (k, m))
+    return shapes
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+@pytest.mark.parametrize("steps", [2, 3, 5])
+def test_many_small_matrices_fused_gram_equals_single(ns_form, steps):
+    """A call with at least one small matrix per apply block forms each next
+    iteration's R inside the apply (whole matrices per block); a single-matrix
+    call keeps the separate gram launch. Both give the same bits."""
+    shapes = _many_small_shapes(300, 4242 + steps)
+    print(f"fused gram {ns_form} steps={steps}: {len(shapes)} small matrices", flush=True)
+    gs = [quarters(s, 5000 + i).to(DEV) for i, s in enumerate(shapes)]
+    outs = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shapes]
+    _lib.newton_schulz_into(list(zip(gs, outs)), ns_form=ns_form, ns_steps=steps)
+    for i, (g, o) in enumerate(zip(gs, outs)):
+        single = torch.empty_like(o)
+        _lib.newton_schulz_into([(g, single)], ns_form=ns_form, ns_steps=steps)
+        assert torch.equal(o, single), (i, tuple(g.shape))
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+def test_many_chunks_muon_step_fused_gram(ns_form):
+    """PAN 2's chunked QKV group with enough chunks for the fused gram (320
+    row blocks of 128 x 256): momentum bit-exact, every chunk's update within
+    the gate of the fp64 oracle, as with a few chunks."""
+    import pan2_amd.optim.patch_muon as pm
+
+    n_chunks, rows, cols = 320, 128, 256
+    lr, wd = 0.02, 0.01
+    p0 = seeded((n_chunks * rows, cols), 15, 0.02)
+    g0 = seeded((n_chunks * rows, cols), 16, 1e-3)
+    b0 = seeded((n_chunks * rows, cols), 17, 1e-3)
+    p = torch.nn.Parameter(p0.to(DEV).clone())
+    p.grad = g0.to(DEV)
+    opt = torch.optim.Muon([{"params": [p], "adjust_lr_fn": ("match_rms_adamw", 0, n_chunks)}],
+                           lr=torch.tensor(lr, device=DEV), weight_decay=wd, adjust_lr_fn="match_rms_adamw")
+    opt.state[p]["momentum_buffer"] = b0.to(DEV).clone()
+    saved = pm.NS_FORM
+    pm.patch_muon(ns_form=ns_form)
+    try:
+        opt.step()
+    finally:
+        pm.NS_FORM = saved
+    torch.cuda.synchronize()
+    got = p.detach().cpu().numpy().astype(np.float64)
+    buf = opt.state[p]["momentum_buffer"].cpu().numpy()
+    ratio = muon_ref.adjust_lr_ratio("match_rms_adamw", (rows, cols))
+    pf, gf = p0.numpy(), g0.numpy()
+    worst = 0.0
+    for k in range(n_chunks):
+        sl = slice(k * rows, (k + 1) * rows)
+        _, ref_b, ref_o = muon_ref.muon_step(pf[sl], gf[sl], b0.numpy()[sl], lr=lr, weight_decay=wd,
+                                             ns_precision="fp64")
+        assert np.array_equal(buf[sl], ref_b), "momentum must be bit-exact"
+        o_got = (pf[sl].astype(np.float64) * (1 - lr * wd) - got[sl]) / (lr * ratio)
+        worst = max(worst, rel_fro(o_got, ref_o))
+    gate = 2e-2 if ns_form == "standard" else 3e-2
+    print(f"{ns_form}: worst chunk rel-Frobenius {worst:.3e} (gate {gate})", flush=True)
+    assert worst <= gate
