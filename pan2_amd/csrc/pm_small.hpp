@@ -444,6 +444,26 @@ __device__ __forceinline__ int xt_off(int k, int n) {
   return k * 128 + ((((n >> 3) & 7) ^ (((k >> 3) & 3) << 1)) << 4) + (n & 7) * 2;
 }
 
+// The MFMA B fragment of columns n0 .. n0+15 (n0 a multiple of 16) for k =
+// k0 .. k0+7 (k0 a multiple of 8) of a unit stored as xt_off lays it out:
+// lane 16g + i gets X[k0 + j][n0 + i], j = 0..7. ds_read_b64_tr_b16 gives lane
+// 4a + b of each 16-lane group element b of the 8 bytes that lanes a, a+4,
+// a+8 and a+12 of the group address (measured on the device), so source lane
+// s of the group points at row k0 + 4h + s/4, columns n0 + 4(s%4) .. +3, and
+// the two reads (h = 0, 1) return 4 consecutive k each.
+__device__ __forceinline__ bf16x8 sm_xcol(const char* xs, int k0, int n0, int r16) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  s16x4 v[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(xs + xt_off(k0 + 4 * h + (r16 >> 2), n0 + 4 * (r16 & 3))));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 w = {v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
 // Param elements r, c0 .. c0+3 of a small matrix's FINAL: whether the row is
 // in bounds, and whether the 4 elements are one aligned vector.
 struct Quad4 {
@@ -789,17 +809,9 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
     auto& d = descs[kw.m];
     const int n0 = 64 * kw.lu;  // the unit's first column of X
     const bool wide = kFinal && !d.trans;
-    // the MFMA fragment of X column n for k-step s (k = 32s + 8g .. +7), read
-    // transposed from the unit, element by element; for these k the swizzle
-    // of xt_off is (n/8 % 8) ^ 2g whatever s and e are
-    auto xcol = [&](int s, int n) {
-      typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-      const char* base = xs + 8 * g * 128 + ((((n >> 3) & 7) ^ (2 * g)) << 4) + (n & 7) * 2;
-      u16x8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = *(const uint16_t*)(base + (32 * s + e) * 128);
-      return __builtin_bit_cast(bf16x8, v);
-    };
+    // the MFMA fragment of X column n = n0 + lane%16 for k-step s (k = 32s +
+    // 8g .. +7), read transposed from the unit by two transposed LDS reads
+    auto xcol = [&](int s, int n0) { return sm_xcol(xs, 32 * s + 8 * g, n0, r16); };
     f32x4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -807,7 +819,7 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
       // Xᵀ S: acc[i] = rows n = 16wc + 4g .. +3 (of Xᵀ) of column m = 64wr + 16i + lane%16
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 xa = xcol(s, 16 * wc + r16);
+        const bf16x8 xa = xcol(s, 16 * wc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = mfma_bf16(xa, sa[i][s], acc[i]);
       }
@@ -815,7 +827,7 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
       // S X: acc[i] = rows m = 64wr + 16i + 4g .. +3 of column n = 16wc + lane%16
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 xb = xcol(s, 16 * wc + r16);
+        const bf16x8 xb = xcol(s, 16 * wc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = mfma_bf16(sa[i][s], xb, acc[i]);
       }
