@@ -56,6 +56,23 @@ def test_noalloc_matches_workspace_step_twice(ns_form):
             assert not torch.equal(got[0][i], make_state(shapes, 100 + k, pdt)[0][i])  # the step moved it
 
 
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+def test_noalloc_many_small_matrices_fused_gram(ns_form):
+    """Enough small matrices for the fused gram (each apply forms the next R):
+    the same bits from the scratch as from a workspace."""
+    shapes = [(128, 256)] * 150 + [(200, 96)] * 150
+    lr = torch.tensor(0.02, device=DEV)
+    print(f"noalloc fused gram {ns_form}: {len(shapes)} small matrices", flush=True)
+    ref = make_state(shapes, 300, torch.bfloat16)
+    got = make_state(shapes, 300, torch.bfloat16)
+    step(ref, noalloc=False, lr=lr, ns_form=ns_form)
+    step(got, noalloc=True, lr=lr, ns_form=ns_form)
+    torch.cuda.synchronize()
+    for i in range(len(shapes)):
+        assert torch.equal(got[0][i], ref[0][i]), f"param {i}"
+        assert torch.equal(got[2][i], ref[2][i]), f"momentum {i}"
+
+
 def test_noalloc_rejects_a_matrix_beyond_the_scratch_untouched():
     """A matrix whose workspace exceeds the scratch fails with PM_EWORKSPACE
     before anything is enqueued: the other matrix of the call is not stepped."""
