@@ -115,15 +115,21 @@ def build_state(shapes, config, device, seed=1234):
 
 GEMM_KERNEL = "pm_ns_gemm_kernel"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
+# kernels whose HBM traffic per launch bench.py reports: the name in the
+# profiler's CSV (a prefix of the demangled name) and the summary file's stem
+TRAFFIC_KERNELS = {
+    "gemm": ("pm_ns_gemm_kernel", "pm_ns_gemm_kernel"),
+    "small_update": ("pm_small_apply_kernel<2, 1, ", "pm_small_apply_kernel_update"),
+}
 
 
-def traffic_path(workload: str) -> str:
-    return os.path.join(ROOT, "profiles", f"{GEMM_KERNEL}_{workload}_traffic.json")
+def traffic_path(workload: str, kernel: str = "gemm") -> str:
+    return os.path.join(ROOT, "profiles", f"{TRAFFIC_KERNELS[kernel][1]}_{workload}_traffic.json")
 
 
-def traffic_bytes(workload: str):
-    """HBM bytes per GEMM launch from the committed counter summary, or None."""
-    path = traffic_path(workload)
+def traffic_bytes(workload: str, kernel: str = "gemm"):
+    """HBM bytes per launch of the kernel from the committed counter summary, or None."""
+    path = traffic_path(workload, kernel)
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -144,9 +150,11 @@ def _counter_by_dispatch(path: str, counter: str) -> dict:
 
 
 def traffic_summary(args) -> int:
-    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the GEMM launches, each
-    scaled by what the same counter reads for the calibration copy (copy_mib MiB
-    read and written). Writes the JSON that bench.py reports as traffic."""
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the launches of
+    --traffic-kernel (the GEMM engine by default), each scaled by what the same
+    counter reads for the calibration copy (copy_mib MiB read and written).
+    Writes the JSON that bench.py reports as traffic."""
+    kname = TRAFFIC_KERNELS[args.traffic_kernel][0]
     if not (args.fetch_csv and args.write_csv and args.copy_mib):
         print("--traffic-summary needs --fetch-csv, --write-csv and --copy-mib", file=sys.stderr)
         return 2
@@ -158,16 +166,16 @@ def traffic_summary(args) -> int:
         # (the counter may read a fixed fraction of the bytes: that fraction is
         # the scale)
         copies = [v for (d, k), v in sorted(vals.items(), key=lambda kv: int(kv[0][0])) if COPY_KERNEL in k][-3:]
-        gemm = [v for (d, k), v in vals.items() if GEMM_KERNEL in k]
+        gemm = [v for (d, k), v in vals.items() if kname in k]
         if not copies or not gemm:
-            print(f"{counter}: no calibration copy or no GEMM dispatches in {path}", file=sys.stderr)
+            print(f"{counter}: no calibration copy or no {kname} dispatches in {path}", file=sys.stderr)
             return 1
         copy_kib = sum(copies) / len(copies)
         scale = known_kib / copy_kib
         result[counter] = {"copy_kib": copy_kib, "scale": scale, "gemm_launches": len(gemm),
                            "gemm_kib_mean_raw": sum(gemm) / len(gemm),
                            "gemm_bytes_mean": sum(gemm) / len(gemm) * scale * 1024.0}
-    out = {"kernel": GEMM_KERNEL, "copy_mib": args.copy_mib,
+    out = {"kernel": kname, "copy_mib": args.copy_mib,
            "bytes_per_launch": result["FETCH_SIZE"]["gemm_bytes_mean"] + result["WRITE_SIZE"]["gemm_bytes_mean"],
            "fetch": result["FETCH_SIZE"], "write": result["WRITE_SIZE"]}
     with open(args.traffic_summary, "w") as f:
@@ -423,6 +431,9 @@ def main() -> int:
                          "per GEMM launch (needs --fetch-csv, --write-csv, --copy-mib)")
     ap.add_argument("--fetch-csv")
     ap.add_argument("--write-csv")
+    ap.add_argument("--traffic-kernel", default="gemm", choices=sorted(TRAFFIC_KERNELS),
+                    help="--traffic-summary: whose launches (gemm: the NS GEMM engine; small_update: the small-matrix "
+                         "UPDATE apply)")
     ap.add_argument("--probe", choices=("ns", "bmm", "ceiling"),
                     help="counter probe instead of the Muon step: 'ns' runs Newton-Schulz alone on 16 x 5120^2 "
                          "bf16 matrices through pm_newton_schulz, 'bmm' the same 16 x 5120^3 products through "
@@ -523,8 +534,8 @@ def main() -> int:
         up_bytes = sum(4.0 * um * un * r["n_matrices"] for r in ups)
         gbs = up_bytes / (up_ms * 1e-3) / 1e9 if up_ms > 0 else 0.0
         roofline = {"kernel": "pm_small_apply_kernel<UPDATE>", "bound": "hbm", "achieved": round(gbs, 1),
-                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                    "bytes_per_element": 4, "launches": len(ups),
+                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                    "traffic": traffic_bytes(name, "small_update"), "bytes_per_element": 4, "launches": len(ups),
                     "avg_launch_ms": round(up_ms / max(1, len(ups)), 3)}
     else:
         roofline = {
