@@ -481,13 +481,14 @@ int run_gram(Launcher& L, const pm_hparams* hp, int max_mp) {
 // core launch also forms that launch's R from the X' it writes, so the core
 // launch reads R (32 KiB a matrix) instead of X' (256 B per column). The fused
 // apply gives each block whole matrices, so a group of few long matrices keeps
-// the separate gram, which spreads one matrix over many blocks.
-int run_small(Launcher& L, const pm_hparams* hp, bool fused) {
+// the separate gram, which spreads one matrix over many blocks. pro_gram: the
+// prologue (pm_small_prologue_kernel) has formed the first R as well.
+int run_small(Launcher& L, const pm_hparams* hp, bool fused, bool pro_gram) {
   const int steps = hp->ns_steps;
   if (hp->ns_form != NS_GRAM) {
     const Coeffs co{hp};
     for (int it = 0; it < steps; ++it) {
-      const bool r_in = fused && it > 0, last = it + 1 == steps;
+      const bool r_in = it > 0 ? fused : pro_gram, last = it + 1 == steps;
       int rc = L.small_core(it & 1, it == 0, it, 0, it, r_in);
       if (!rc) rc = L.small_apply(co.at(it).a, it & 1, it == 0, last, it, fused && !last);
       if (rc) return rc;
@@ -496,7 +497,7 @@ int run_small(Launcher& L, const pm_hparams* hp, bool fused) {
   }
   const int reset = gram_reset(steps);
   const int seg1 = reset > 0 ? reset : steps;
-  int rc = L.small_core(0, true, 0, seg1, 0);
+  int rc = L.small_core(0, true, 0, seg1, 0, pro_gram);
   if (!rc) rc = L.small_apply(0.0f, 0, true, seg1 == steps, seg1 - 1, fused && seg1 < steps);
   if (!rc && seg1 < steps) {
     rc = L.small_core(1, false, seg1, steps - seg1, seg1, fused);
@@ -601,11 +602,43 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   const int32_t* dfull = (const int32_t*)(ws + ((char*)full - host.data()));
   int32_t* dqueues = (int32_t*)(ws + ((const char*)queues - host.data()));
 
+  // Small matrices: with many of them the apply takes the fused gram (one
+  // matrix per apply block at least, none longer than twice a block's even
+  // share of the units), and the prologue forms the first R as well when every
+  // matrix's prologue partials fit its LDS.
+  bool fused = false, pro_gram = false;
+  if (small) {
+    int32_t longest = 0, parts = 0;
+    for (int i = 0; i < count; ++i) {
+      longest = std::max(longest, full[i + 1] - full[i]);
+      parts = std::max(parts, pro[i + 1] - pro[i]);
+    }
+    const int grid = gemm_grid(full[count]);
+    fused = count >= grid && (int64_t)longest * grid <= 2 * (int64_t)full[count];
+    pro_gram = fused && parts <= kSmProParts;
+  }
+
   ProArgs pa{ddesc, dpro, count, mode, hp->momentum, hp->nesterov, small ? XL_SMALL : ((kWsLayout & kTiledX) ? XL_PANEL : XL_ROW), 0};
-  hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
-  timing_mark(stream, PM_K_PROLOGUE, group, -1, count, 0.0, b_pro);
-  hipLaunchKernelGGL(pm_norm_kernel, dim3(count), dim3(kThreads), 0, stream, ddesc, hp->eps);
-  timing_mark(stream, PM_K_NORM, group, -1, count, 0.0, 0.0);
+  if (pro_gram) {
+    // instantiated for the first matrix's dtypes (a matrix of other dtypes
+    // takes the kernel's element-wise loads)
+    const bool g32 = items[0].desc.g_dt == PM_DTYPE_F32, m32 = items[0].desc.m_dt == PM_DTYPE_F32;
+    const dim3 grid(count), block(kGemmThreads);
+    if (g32 && m32)
+      hipLaunchKernelGGL((pm_small_prologue_kernel<true, true>), grid, block, 0, stream, pa, hp->eps, 0);
+    else if (g32)
+      hipLaunchKernelGGL((pm_small_prologue_kernel<true, false>), grid, block, 0, stream, pa, hp->eps, 0);
+    else if (m32)
+      hipLaunchKernelGGL((pm_small_prologue_kernel<false, true>), grid, block, 0, stream, pa, hp->eps, 0);
+    else
+      hipLaunchKernelGGL((pm_small_prologue_kernel<false, false>), grid, block, 0, stream, pa, hp->eps, 0);
+    timing_mark(stream, PM_K_PROLOGUE, group, -1, count, f_gram, b_pro);
+  } else {
+    hipLaunchKernelGGL(pm_prologue_kernel, dim3(pro[count]), dim3(kThreads), 0, stream, pa);
+    timing_mark(stream, PM_K_PROLOGUE, group, -1, count, 0.0, b_pro);
+    hipLaunchKernelGGL(pm_norm_kernel, dim3(count), dim3(kThreads), 0, stream, ddesc, hp->eps);
+    timing_mark(stream, PM_K_NORM, group, -1, count, 0.0, 0.0);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prologue launch");
 
@@ -632,14 +665,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   L.f_sym = f_sym;
   L.f_upd = f_upd;
   L.coeffs = (const float*)(ws + ((char*)coeffs - host.data()));
-  if (items[0].plan.small) {
-    // fused gram: at least one matrix per apply block, none longer than
-    // twice a block's even share of the units
-    int32_t longest = 0;
-    for (int i = 0; i < count; ++i) longest = std::max(longest, full[i + 1] - full[i]);
-    const bool fused = count >= L.full_grid && (int64_t)longest * L.full_grid <= 2 * (int64_t)full[count];
-    return run_small(L, hp, fused);
-  }
+  if (small) return run_small(L, hp, fused, pro_gram);
   return form == NS_GRAM ? run_gram(L, hp, max_mp) : run_standard(L, hp);
 }
 

@@ -263,20 +263,20 @@ __device__ __forceinline__ void sm_gram_acc(const char* src, f32x4 (&acc)[4][2],
   }
 }
 
-// R = bf16(acc) written row-major (128 x 128) to global memory, through the
-// LDS matrix T: elements on and above the diagonal at (p, q) and (q, p), as
-// sm_finish writes them with alpha = 1, beta = 0 (the same expression, so the
-// same bits), then whole rows out with 16-byte stores. Every wave of the block
+// R = bf16(alpha·acc) written row-major (128 x 128) to global memory, through
+// the LDS matrix T: elements on and above the diagonal at (p, q) and (q, p),
+// as sm_finish writes them with beta = 0 (the same expression, so the same
+// bits), then whole rows out with 16-byte stores. Every wave of the block
 // calls it: it begins with a barrier (every wave's earlier reads of T's tiles
 // have completed: their MFMAs consumed them) and ends with one (every read of T
 // is done, so the tiles may be written again). The barriers are bare: a
 // __syncthreads fence would also wait for the copies in flight.
 __device__ __forceinline__ void sm_gram_store(uint16_t* Rg, const SmMat& T, const f32x4 (&acc)[4][2], int r0, int c0,
-                                              int lane) {
+                                              int lane, float alpha = 1.0f) {
 #pragma clang fp contract(off)
   const int g = lane >> 4;
   const int rh = r0 >> 6, ch = c0 >> 6, cr = c0 & 63;
-  const float alpha = 1.0f, beta = 0.0f;
+  const float beta = 0.0f;
   u16x4 o[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -433,6 +433,417 @@ __global__ __launch_bounds__(kGemmThreads, kSmRing / RING) void pm_small_core_ke
     const SmMat out{out_q ? Q.h0 : Z.h0, out_q ? Q.h1 : Z.h1};
     glb_store16(S + r * kSm + 8 * c, lds_load16(sm_at(out, r >> 6, r & 63, c)));
   }
+}
+
+// ============================================================ prologue + first gram
+// Largest prologue partial count per matrix (2 tile rows x 1024 runs: a long
+// side of 262144) that pm_small_prologue_kernel keeps in LDS.
+constexpr int kSmProParts = 2048;
+
+// The descriptor fields pm_small_prologue_kernel's tile loop reads, loaded
+// once into scalar registers: read through the descriptor after the loop's
+// stores, they would be reloaded with vector loads every tile.
+struct ProMat {
+  const void* grad;
+  void* mom;
+  uint16_t* X;
+  int64_t g_ld, m_ld;
+  int32_t rows, cols, g_dt, m_dt, trans;
+};
+__device__ __forceinline__ int32_t uni32(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ ProMat pro_mat(const MatDesc& d) {
+  ProMat q;
+  q.grad = (const void*)uni64((int64_t)d.grad);
+  q.mom = (void*)uni64((int64_t)d.mom);
+  q.X = (uint16_t*)uni64((int64_t)d.X[0]);
+  q.g_ld = uni64(d.g_ld);
+  q.m_ld = uni64(d.m_ld);
+  q.rows = uni32(d.rows);
+  q.cols = uni32(d.cols);
+  q.g_dt = uni32(d.g_dt);
+  q.m_dt = uni32(d.m_dt);
+  q.trans = uni32(d.trans);
+  return q;
+}
+
+// A run of 8 elements' gradient and momentum as loaded (G32 / M32: fp32,
+// else bf16), for the runs that take the vector path: pm_small_prologue_kernel
+// issues the loads of four runs before the arithmetic of any of them.
+template <bool G32, bool M32>
+struct ProRaw {
+  u32x4 g[G32 ? 2 : 1];
+  u32x4 m[M32 ? 2 : 1];
+};
+
+// The 16-byte loads pm_prologue_kernel makes for param row pr, columns
+// pc .. pc+7 (gvec / mvec: the vector path is allowed and the dtype is the
+// template's).
+template <bool G32, bool M32>
+__device__ __forceinline__ void pro_fetch8(const ProMat& d, bool step, int pr, int pc, bool gvec, bool mvec,
+                                           ProRaw<G32, M32>& raw) {
+  const bool full = pr < d.rows && d.cols - pc >= 8;
+  raw = ProRaw<G32, M32>{};  // defined where the loads are skipped
+  // global_ rather than flat loads: a flat load also counts in lgkmcnt, and
+  // the compiler then drains every counter before using any of them
+  if (full && gvec) {
+    const glb_u32x4* p = (const glb_u32x4*)((const char*)d.grad + ((int64_t)pr * d.g_ld + pc) * (G32 ? 4 : 2));
+    raw.g[0] = p[0];
+    if constexpr (G32) raw.g[1] = p[1];
+  }
+  if (full && step && mvec) {
+    const glb_u32x4* p = (const glb_u32x4*)((const char*)d.mom + ((int64_t)pr * d.m_ld + pc) * (M32 ? 4 : 2));
+    raw.m[0] = p[0];
+    if constexpr (M32) raw.m[1] = p[1];
+  }
+}
+
+// 8 floats from a run's raw vector (load8's conversions).
+template <bool F32, int N>
+__device__ __forceinline__ void pro_unpack8(const u32x4 (&v)[N], float (&x)[8]) {
+  if constexpr (F32) {
+    // through scalars: this clang's __builtin_bit_cast of a vector element
+    // (v[i][e]) reads element 0 whatever e is
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = v[0][e], hi = v[N - 1][e];
+      x[e] = __builtin_bit_cast(float, lo);
+      x[4 + e] = __builtin_bit_cast(float, hi);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf2f((uint16_t)(v[0][e] & 0xffff));
+      x[2 * e + 1] = bf2f((uint16_t)(v[0][e] >> 16));
+    }
+  }
+}
+
+// load_elem / store_elem as global_ accesses (flat ones would make the
+// compiler drain every counter at each later wait in the kernel).
+__device__ __forceinline__ float load_elem_g(const void* p, int32_t dt, int64_t i) {
+  typedef const __attribute__((address_space(1))) float gf;
+  typedef const __attribute__((address_space(1))) uint16_t gh;
+  return dt == DT_F32 ? ((gf*)p)[i] : bf2f(((gh*)p)[i]);
+}
+__device__ __forceinline__ void store_elem_g(void* p, int32_t dt, int64_t i, float v) {
+  typedef __attribute__((address_space(1))) float gf;
+  typedef __attribute__((address_space(1))) uint16_t gh;
+  if (dt == DT_F32) ((gf*)p)[i] = v;
+  else ((gh*)p)[i] = f2bf(v);
+}
+
+// pm_prologue_kernel's arithmetic on one run of 8 elements of param row pr,
+// columns pc .. pc+7, with its vector loads already issued into raw
+// (pro_fetch8 with the same gvec / mvec); runs off the vector path load
+// element by element here. The momentum update is stored back and u (the
+// Nesterov blend, or the gradient in MODE_NS) is rounded to bf16 and packed;
+// ss accumulates the squares of the rounded values in element order, and
+// elements outside the parameter are zeros of X. mvec_any: the caller's
+// strides and bases allow the momentum's 16-byte stores, whatever its dtype.
+// FAST: the matrix allows the vector path for every run inside it (gvec,
+// mvec in MODE_STEP, and a column count that is a multiple of 8), so every
+// run is either whole or padding, and raw comes from sm_pro_fetch_buf (zeros
+// for padding): no element loads remain.
+template <bool FAST, bool G32, bool M32>
+__device__ __forceinline__ u32x4 pro_finish8(const ProArgs& args, const ProMat& d, int pr, int pc, bool gvec,
+                                             bool mvec, bool mvec_any, const ProRaw<G32, M32>& raw, float& ss) {
+#pragma clang fp contract(off)
+  const float mu = args.mu, omu = 1.0f - args.mu;
+  const bool step = args.mode == MODE_STEP;
+  const bool in_row = pr < d.rows;
+  const int valid = d.cols - pc;  // elements of the run inside the parameter
+  const bool full = in_row && valid >= 8;
+  float u[8];
+  float g[8];
+  // The element loads of the other runs complete inside their branch (the
+  // empty asm uses them there): loads still pending at the join would make
+  // the vector path wait for every load in flight, the next run's included.
+  if (FAST || (full && gvec)) {
+    pro_unpack8<G32>(raw.g, g);  // FAST: zeros outside the parameter
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      g[e] = (in_row && e < valid) ? load_elem_g(d.grad, d.g_dt, (int64_t)pr * d.g_ld + pc + e) : 0.0f;
+      asm volatile("" : "+v"(g[e]));
+    }
+  }
+  if (step) {
+    float m[8];
+    const int64_t mo = (int64_t)pr * d.m_ld + pc;
+    if (FAST || (full && mvec)) {
+      pro_unpack8<M32>(raw.m, m);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        m[e] = (in_row && e < valid) ? load_elem_g(d.mom, d.m_dt, mo + e) : 0.0f;
+        asm volatile("" : "+v"(m[e]));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float nm = mu * m[e] + omu * g[e];
+      m[e] = nm;
+      u[e] = args.nesterov ? omu * g[e] + mu * nm : nm;
+    }
+    // store8's stores, the 16-byte ones as global_ stores
+    if (in_row && mvec_any && valid >= 8) {
+      if (d.m_dt == DT_F32) {
+        typedef __attribute__((address_space(1))) f32x4 glb_f32x4;
+        glb_f32x4* q = (glb_f32x4*)((float*)d.mom + mo);
+        q[0] = (f32x4){m[0], m[1], m[2], m[3]};
+        q[1] = (f32x4){m[4], m[5], m[6], m[7]};
+      } else {
+        u32x4 a;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = (uint32_t)f2bf(m[2 * e]) | ((uint32_t)f2bf(m[2 * e + 1]) << 16);
+        *(glb_u32x4*)((uint16_t*)d.mom + mo) = a;
+      }
+    } else if (!FAST && in_row) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < valid) store_elem_g(d.mom, d.m_dt, mo + e, m[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) u[e] = g[e];
+  }
+  u32x4 packed;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint16_t lo = (in_row && 2 * e < valid) ? f2bf(u[2 * e]) : (uint16_t)0;
+    const uint16_t hi = (in_row && 2 * e + 1 < valid) ? f2bf(u[2 * e + 1]) : (uint16_t)0;
+    const float flo = bf2f(lo), fhi = bf2f(hi);
+    ss += flo * flo;
+    ss += fhi * fhi;
+    packed[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  return packed;
+}
+
+// The param origin of tile tj of X rows 64·half .. 64·half+63, and this
+// thread's place in it (thread t of the half: rows t/8 and t/8 + 32 of the
+// tile, columns 8(t%8) .. +7, as pm_prologue_kernel's thread t). t is rebuilt
+// from the lane index at each use, so per-lane offsets are not hoisted out of
+// the tile loop (where they would all stay live).
+struct ProPos {
+  int t, cg, pr0, pc0;
+};
+__device__ __forceinline__ ProPos sm_pro_pos(const ProMat& d, int tj, int half, int wq) {
+  ProPos q;
+  q.t = wq * 64 + lane_id();
+  q.cg = (q.t & 7) * 8;
+  q.pr0 = d.trans ? tj * kProTile : half * kProTile;
+  q.pc0 = d.trans ? half * kProTile : tj * kProTile;
+  return q;
+}
+
+// The loads of half h of tile tj (param row pr0 + t/8 + 32h) into raw.
+template <bool G32, bool M32>
+__device__ __forceinline__ void sm_pro_fetch(const ProMat& d, bool step, int tj, int h, int half, int wq, bool gvec,
+                                             bool mvec, ProRaw<G32, M32>& raw) {
+  const ProPos q = sm_pro_pos(d, tj, half, wq);
+  pro_fetch8(d, step, q.pr0 + (q.t >> 3) + 32 * h, q.pc0 + q.cg, gvec, mvec, raw);
+}
+
+// sm_pro_fetch for a FAST matrix, as buffer loads issued by every lane: a run
+// outside the parameter (padding rows or columns) gets an offset beyond the
+// resource's range, whose loads return zeros. Loads issued under a branch
+// would leave the compiler unsure how many loads follow a register set's,
+// and it would then wait for all of them. rg / rm cover the gradient and the
+// momentum (extents below 2 GiB).
+template <bool G32, bool M32>
+__device__ __forceinline__ void sm_pro_fetch_buf(const ProMat& d, bool step, __amdgpu_buffer_rsrc_t rg,
+                                                 __amdgpu_buffer_rsrc_t rm, int tj, int h, int half, int wq,
+                                                 ProRaw<G32, M32>& raw) {
+  const ProPos q = sm_pro_pos(d, tj, half, wq);
+  const int pr = q.pr0 + (q.t >> 3) + 32 * h, pc = q.pc0 + q.cg;
+  const bool full = pr < d.rows && d.cols - pc >= 8;
+  const uint32_t og = full ? (uint32_t)(((int64_t)pr * d.g_ld + pc) * (G32 ? 4 : 2)) : 0x80000000u;
+  raw.g[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rg, og, 0, 0));
+  if constexpr (G32) raw.g[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rg, og + 16, 0, 0));
+  if (step) {
+    const uint32_t om = full ? (uint32_t)(((int64_t)pr * d.m_ld + pc) * (M32 ? 4 : 2)) : 0x80000000u;
+    raw.m[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, om, 0, 0));
+    if constexpr (M32) raw.m[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, om + 16, 0, 0));
+  }
+}
+
+// Half h of tile tj (64 columns of X: one gram unit) of a small matrix in a
+// pm_small_prologue_kernel block: pm_prologue_kernel's work on the run of 8
+// elements its thread t takes in that half of the tile (X rows
+// 64·half .. 64·half+63), from the loads in raw; the run's X also goes into
+// LDS unit `unit` (the gram's unit layout: row r, chunk c at chunk
+// c ^ ((r >> 1) & 7)). ss accumulates the thread's squares as
+// pm_prologue_kernel's thread t does (h = 0, then 1, tile by tile).
+template <bool FAST, bool G32, bool M32>
+__device__ __forceinline__ void sm_pro_run(const ProArgs& args, const ProMat& d, char* unit, int tj, int h, int half,
+                                           int wq, bool gvec, bool mvec, bool mvec_any, const ProRaw<G32, M32>& raw,
+                                           float& ss) {
+  const ProPos q = sm_pro_pos(d, tj, half, wq);
+  const int r = (q.t >> 3) + 32 * h;
+  const u32x4 packed = pro_finish8<FAST>(args, d, q.pr0 + r, q.pc0 + q.cg, gvec, mvec, mvec_any, raw, ss);
+  if (!d.trans) {
+    // X row 64·half + r, columns 64·tj + cg .. +7
+    const int xr = half * kProTile + r;
+    glb_store16(d.X + sm_x_off(xr, tj * kProTile + q.cg), packed);
+    lds_store16(unit + xr * 128 + (((q.cg >> 3) ^ ((xr >> 1) & 7)) << 4), packed);
+  } else {
+    // param row pr0 + r is X column 64·tj + r; its columns cg .. cg+7 are X
+    // rows 64·half + cg + e
+    typedef __attribute__((address_space(3))) uint16_t lds_u16;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int xr = half * kProTile + q.cg + e;
+      const uint16_t v = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
+      *(lds_u16*)(unit + xr * 128 + (((r >> 3) ^ ((xr >> 1) & 7)) << 4) + (r & 7) * 2) = v;
+    }
+  }
+}
+
+// A transposed tile's X rows out of LDS: thread t of the half writes X row
+// 64·half + t/4, columns 64·tj + 16·(t%4) .. +15 (the rows the prologue's
+// transposing tile gives pm_prologue_kernel's thread t).
+__device__ __forceinline__ void sm_pro_flush_tr(const ProMat& d, const char* unit, int tj, int half, int wq) {
+  const int t = wq * 64 + lane_id();
+  const int xr = half * kProTile + (t >> 2), rb = (t & 3) * 16;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c8 = (rb >> 3) + h;
+    glb_store16(d.X + sm_x_off(xr, tj * kProTile + 8 * c8),
+                lds_load16(unit + xr * 128 + ((c8 ^ ((xr >> 1) & 7)) << 4)));
+  }
+}
+
+// pm_small_prologue_kernel's pass over the tiles of its matrix (the
+// prologue, the partial sums and the gram's accumulation, run by run).
+template <bool FAST, bool G32, bool M32>
+__device__ __forceinline__ void sm_pro_tiles(const ProArgs& args, const ProMat& pm, char (*units)[kSmUnit], float* parts,
+                                             float* red, float* partials, f32x4 (&acc)[4][2], int nrun, int half,
+                                             int wq, bool gvec, bool mvec, bool mvec_any, __amdgpu_buffer_rsrc_t rg,
+                                             __amdgpu_buffer_rsrc_t rm) {
+  auto fetch = [&](int tj, int h, ProRaw<G32, M32>& raw) {
+    if constexpr (FAST)
+      sm_pro_fetch_buf(pm, args.mode == MODE_STEP, rg, rm, tj, h, half, wq, raw);
+    else
+      sm_pro_fetch(pm, args.mode == MODE_STEP, tj, h, half, wq, gvec, mvec, raw);
+  };
+  const bool step = args.mode == MODE_STEP;
+  const int wave = 4 * half + wq, lane = lane_id();
+  const int r0 = half * 64, c0 = wq * 32;
+  const int ntiles = nrun * kProRun;
+  // Tiles go in pairs: the four runs of a pair are loaded before any of
+  // their arithmetic, so each thread has four loads in flight at once. (The
+  // compiler waits for every memory operation before using a load's result
+  // whenever stores are pending, so loads issued a run ahead across the
+  // previous run's stores gain nothing.)
+  float ss = 0.0f;
+  for (int tj = 0; tj < ntiles; tj += 2) {
+    const int tt = tj & (kProRun - 1), run = tj / kProRun;
+    ProRaw<G32, M32> r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fetch(tj + (i >> 1), i & 1, r[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sm_pro_run<FAST>(args, pm, units[tt + (i >> 1)], tj + (i >> 1), i & 1, half, wq, gvec, mvec, mvec_any, r[i], ss);
+    if (tt + 2 != kProRun) continue;
+    // ---- end of a 256-column run: the prologue block's partial (its waves'
+    // sums, then (0 + 1) + (2 + 3)) and the run's four units into the gram
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    ss = 0.0f;
+    lds_barrier();  // the run's units and sums are in LDS
+    if (pm.trans) {
+#pragma unroll 1
+      for (int u = 0; u < kProRun; ++u) sm_pro_flush_tr(pm, units[u], run * kProRun + u, half, wq);
+    }
+    if (wq == 0 && lane == 0 && half * nrun + run < kSmProParts) {
+      const float* rh = red + 4 * half;
+      const float part = (rh[0] + rh[1]) + (rh[2] + rh[3]);
+      parts[half * nrun + run] = part;
+      partials[half * nrun + run] = part;
+    }
+    // (the lane index rebuilt for each unit keeps the fragment offsets out of
+    // the registers live across the streaming part)
+#pragma unroll 1
+    for (int u = 0; u < kProRun; ++u) sm_gram_acc(units[u], acc, r0, c0, lane_id());
+    lds_barrier();  // every wave is done with the units and the sums
+  }
+
+}
+
+// One block of 8 waves per small matrix of the group (grid = matrices): the
+// work of pm_prologue_kernel, pm_norm_kernel and the first gram of
+// pm_small_core_kernel (R = s²·X Xᵀ, s = 1/‖X‖) in one pass, so the first core
+// launch reads R (r_in) instead of X.
+// Waves 0-3 and 4-7 run the prologue blocks of X rows 0-63 and 64-127 of each
+// 256-column run side by side, thread for thread as pm_prologue_kernel runs
+// them (the same elements in the same order, so the momentum, X and the
+// partial sums are the same bits); the run's four 64-column units of X also
+// go to LDS, where every wave adds its part of X Xᵀ with sm_gram_acc, unit by
+// unit in column order as the core kernel's gram does. The partials reduce as
+// in pm_norm_kernel, and R = bf16(s²·acc) goes to S[so] as sm_finish would
+// round it. The caller keeps pro_tiles <= kSmProParts.
+// G32 / M32: the dtypes whose runs take the vector path (fp32 or bf16 grads
+// and momentum; a matrix of the other dtype loads element by element).
+template <bool G32, bool M32>
+__global__ __launch_bounds__(kGemmThreads, 4) void pm_small_prologue_kernel(ProArgs args, float eps, int32_t so) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) char units[kProRun][kSmUnit];
+  __shared__ float parts[kSmProParts];
+  __shared__ float red[kGemmThreads / 64];
+
+  const MatDesc& d = args.descs[blockIdx.x];
+  const ProMat pm = pro_mat(d);
+  const int wave = wave_id(), lane = lane_id();
+  const int half = wave >> 2, wq = wave & 3;
+  const int r0 = (wave >> 2) * 64, c0 = (wave & 3) * 32;
+  const int nrun = uni32(d.Np) / (kProTile * kProRun), ntiles = nrun * kProRun;
+  float* const partials = (float*)uni64((int64_t)d.partials);
+  const bool step = args.mode == MODE_STEP;
+  const bool mvec_any = step && vec_ok(pm.mom, pm.m_dt, pm.m_ld);
+  const bool gvec = vec_ok(pm.grad, pm.g_dt, pm.g_ld) && pm.g_dt == (G32 ? DT_F32 : DT_BF16);
+  const bool mvec = mvec_any && pm.m_dt == (M32 ? DT_F32 : DT_BF16);
+
+  f32x4 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // FAST: every run is whole or padding, and the gradient and momentum fit
+  // buffer resources (extents below 2 GiB)
+  const int64_t gext = ((int64_t)(pm.rows - 1) * pm.g_ld + pm.cols) * (G32 ? 4 : 2);
+  const int64_t mext = step ? ((int64_t)(pm.rows - 1) * pm.m_ld + pm.cols) * (M32 ? 4 : 2) : 0;
+  const bool fast = gvec && (!step || mvec) && (pm.cols & 7) == 0 && gext < 0x7fff0000 && mext < 0x7fff0000;
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void*)pm.grad, (short)0, fast ? (int)gext : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(pm.mom, (short)0, fast ? (int)mext : 0, 0x00020000);
+  if (fast)
+    sm_pro_tiles<true, G32, M32>(args, pm, units, parts, red, partials, acc, nrun, half, wq, gvec, mvec, mvec_any, rg, rm);
+  else
+    sm_pro_tiles<false, G32, M32>(args, pm, units, parts, red, partials, acc, nrun, half, wq, gvec, mvec, mvec_any, rg, rm);
+
+  // ---- the norm: pm_norm_kernel's reduction, by waves 0-3
+  float s = 0.0f;
+  if (half == 0)
+    for (int i = threadIdx.x; i < min(d.pro_tiles, kSmProParts); i += kThreads) s += parts[i];
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  lds_barrier();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float nrm = sqrtf(tot);
+  nrm = (nrm != nrm) ? nrm : fmaxf(nrm, eps);
+  const float inv = 1.0f / nrm;
+  if (threadIdx.x == 0) {
+    d.scales[0] = inv * inv;
+    d.scales[1] = inv;
+  }
+  // ---- R = s²·X Xᵀ to S[so], staged in units 0 and 1
+  sm_gram_store(d.S[so], SmMat{units[0], units[1]}, acc, r0, c0, lane, inv * inv);
 }
 
 // A unit of X in LDS, laid out as in HBM (sm_x_off): kSm rows (k) of 64

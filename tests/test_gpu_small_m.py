@@ -316,3 +316,37 @@ def test_many_chunks_muon_step_fused_gram(ns_form):
     gate = 2e-2 if ns_form == "standard" else 3e-2
     print(f"{ns_form}: worst chunk rel-Frobenius {worst:.3e} (gate {gate})", flush=True)
     assert worst <= gate
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+@pytest.mark.parametrize("dtypes", ["bf16_grad_f32_mom", "f32_grad_f32_mom", "bf16_grad_bf16_mom", "mixed_grads"])
+def test_many_small_muon_steps_fused_equal_single(ns_form, dtypes):
+    """A Muon step over 300 small matrices (short sides 1..128, long sides
+    with and without a multiple of 8, wide and tall) takes the fused path:
+    the prologue forms the first gram too (pm_small_prologue_kernel, its
+    whole-vector loop where a matrix's strides and columns allow, element
+    loads elsewhere). Single-matrix calls keep the separate prologue, norm
+    and gram. Params and momentum must be equal bit for bit."""
+    shapes = _many_small_shapes(300, 9000 + len(dtypes))
+    rng = np.random.default_rng(77)
+    g_dts, m_dt = {
+        "bf16_grad_f32_mom": ([torch.bfloat16] * 300, torch.float32),
+        "f32_grad_f32_mom": ([torch.float32] * 300, torch.float32),
+        "bf16_grad_bf16_mom": ([torch.bfloat16] * 300, torch.bfloat16),
+        "mixed_grads": ([torch.float32 if rng.integers(2) else torch.bfloat16 for _ in range(300)], torch.float32),
+    }[dtypes]
+    print(f"fused prologue {ns_form} {dtypes}: {len(shapes)} small matrices", flush=True)
+    lr, wd = 0.02, 0.01
+    kw = dict(lr=lr, weight_decay=wd, momentum=0.95, nesterov=True, ns_coefficients=(3.4445, -4.7750, 2.0315),
+              ns_steps=5, eps=1e-7, ns_form=ns_form)
+    p0 = [seeded(s, 100 + i, 0.02).to(DEV, torch.bfloat16) for i, s in enumerate(shapes)]
+    g0 = [seeded(s, 500 + i, 1e-3).to(DEV, g_dts[i]) for i, s in enumerate(shapes)]
+    b0 = [seeded(s, 900 + i, 1e-3).to(DEV, m_dt) for i, s in enumerate(shapes)]
+    ratios = [1.0] * len(shapes)
+    ps, bs = [p.clone() for p in p0], [b.clone() for b in b0]
+    _lib.muon_step(ps, g0, bs, ratios, **kw)
+    for i in range(len(shapes)):
+        p1, b1 = p0[i].clone(), b0[i].clone()
+        _lib.muon_step([p1], [g0[i]], [b1], [1.0], **kw)
+        assert torch.equal(bs[i], b1), ("momentum", i, shapes[i])
+        assert torch.equal(ps[i], p1), ("param", i, shapes[i])

@@ -96,18 +96,22 @@ def test_small_kernels_keep_lds_in_lds(asm):
     with ds_ instructions (a pointer that went through memory turns them into
     flat accesses that wait on both counters). The apply that also forms the
     gram writes and reads its X' tiles with ds_ instructions: a flat access
-    there would also count in vmcnt, whose exact waits the apply relies on."""
+    there would also count in vmcnt, whose exact waits the apply relies on.
+    The prologue that forms the first gram writes its X units to LDS and reads
+    the MFMA fragments back with ds_ instructions."""
     kernels = {}
     for m in re.finditer(r"^(_ZN2pm\d+pm_small_\w+):.*$", asm, flags=re.M):
         body = asm[m.end():]
         kernels[m.group(1)] = body[:body.index(".Lfunc_end")]
-    assert len(kernels) == 6, sorted(kernels)
+    assert len(kernels) == 10, sorted(kernels)
     for name, body in kernels.items():
         assert "scratch_" not in body, name
         if "core_kernel" in name:
             wide_flat = re.findall(r"^\s*flat_(load|store)_dwordx[24]", body, flags=re.M)
             assert not wide_flat, f"{name}: {len(wide_flat)} flat accesses of 8 or 16 bytes"
             assert "ds_read_b128" in body, name
+        if "prologue_kernel" in name:
+            assert "ds_write_b128" in body and "ds_read_b128" in body and "v_mfma" in body, name
     gram_apply = [name for name in kernels if "apply_kernelILi2ELi1ELb1E" in name]
     assert len(gram_apply) == 1, sorted(kernels)
     body = kernels[gram_apply[0]]
