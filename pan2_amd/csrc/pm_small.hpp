@@ -20,6 +20,11 @@
 //                          matrices. Small matrices keep X only, no Xᵀ: the
 //                          apply reads X transposed from LDS.
 //
+// With many matrices in a call, the R a core launch starts from is formed by
+// the kernel that wrote X instead: the UPDATE apply (its X'), and for the
+// first launch pm_small_prologue_kernel, which runs the momentum prologue, the
+// norm and the first gram in one pass. The core launches then read R only.
+//
 // This is the counterpart of the reference's fused batched gram-NS
 // (pan/optim/muon_triton.py:234-345: the gram and the 128 x 128 iteration in
 // one program per matrix, the two Q X applications as batched GEMMs). Every
