@@ -225,9 +225,10 @@ def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
 def probe_ceiling(units: int = 3000) -> int:
     """MFMA ceilings of the GEMM engine's loop on this chip (pan2_amd/csrc/pm_probe.hip):
     MFMA alone; with the engine's LDS fragment reads and barriers (8 waves of
-    128 x 64, then 4 waves of 128 x 128); and the 8-wave loop with the engine's
+    128 x 64, then 4 waves of 128 x 128); the 8-wave loop with the engine's
     global -> LDS copies, from a 64 MiB window per XCD and from one 1 MiB window
-    that stays in L2. One line each, two rounds."""
+    that stays in L2; and MFMA alone with the 32 x 32 x 16 instruction. One
+    line each, two rounds."""
     import ctypes
 
     import torch
@@ -249,7 +250,8 @@ def probe_ceiling(units: int = 3000) -> int:
              (1, 0, 1, "mfma + LDS fragment reads + 2 barriers per 64-deep unit (8 waves of 128x64)"),
              (2, 0, 1, "mfma + LDS fragment reads + 2 barriers per 64-deep unit (4 waves of 128x128)"),
              (3, 64 * mib, 8, "as 1 + the engine's global->LDS copies, a 64 MiB window per XCD"),
-             (3, 1 * mib, 1, "as 1 + the engine's global->LDS copies, one 1 MiB window (L2-resident)")]
+             (3, 1 * mib, 1, "as 1 + the engine's global->LDS copies, one 1 MiB window (L2-resident)"),
+             (4, 0, 1, "mfma only with v_mfma_f32_32x32x16_bf16 (the same 128x64 accumulators as 4x2 blocks)")]
     for _ in range(2):
         for which, span, nwin, name in cases:
             ms, fl = ctypes.c_float(), ctypes.c_double()

@@ -16,7 +16,8 @@
 //      its vmcnt waits before the barriers): 64 KiB per unit per CU, unit u of
 //      a block reading bytes (64 KiB * u) mod span of its window; block b reads
 //      window b mod nwin of the source (nwin = 8 gives each XCD its own window,
-//      shared by its 32 CUs as a tile block shares its panels).
+//      shared by its 32 CUs as a tile block shares its panels);
+//   4  as 0 with v_mfma_f32_32x32x16_bf16 (probe32_kernel).
 // Fragment reads stay inside the first 68 KiB of the 128 KiB LDS array, and
 // copies fill it as the engine's two-unit ring (4 x 32 KiB); each block writes
 // only its own output slots.
@@ -129,6 +130,71 @@ __global__ __launch_bounds__(WAVES * 64, 1) void probe_kernel(float* out, int un
   out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
 }
 
+// Probe 4: as probe 0 with v_mfma_f32_32x32x16_bf16, the 128 x 64 wave tile
+// as 4 x 2 blocks of 32 x 32 (the same 128 accumulators per lane, in AGPRs):
+// a 64-deep unit is 32 MFMAs of twice probe 0's FLOPs, on half the operand
+// register reads per FLOP.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ void mfma32(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__global__ __launch_bounds__(512, 1) void probe32_kernel(float* out, int units) {
+  const int lane = threadIdx.x & 63;
+  bf16x8 af[4], bfr[2];
+  for (int i = 0; i < 4; ++i) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v v = {rnd_pair(lane * 16 + 4 * i, blockIdx.x), rnd_pair(lane * 16 + 4 * i + 1, blockIdx.x),
+                      rnd_pair(lane * 16 + 4 * i + 2, blockIdx.x), rnd_pair(lane * 16 + 4 * i + 3, blockIdx.x)};
+    af[i] = __builtin_bit_cast(bf16x8, v);
+    if (i < 2) {
+      const u32x4v w = {rnd_pair(lane * 16 + 4 * i + 100, blockIdx.x), rnd_pair(lane * 16 + 4 * i + 101, blockIdx.x),
+                        rnd_pair(lane * 16 + 4 * i + 102, blockIdx.x), rnd_pair(lane * 16 + 4 * i + 103, blockIdx.x)};
+      bfr[i] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+  f32x16 acc[4][2];
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j)
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  for (int u = 0; u < units; ++u) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mfma32(acc[i][j], af[i], bfr[j]);
+      asm volatile("" ::"v"(af[0]), "v"(af[1]), "v"(af[2]), "v"(af[3]), "v"(bfr[0]), "v"(bfr[1]));
+    }
+  }
+  asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
+  float sum = 0.0f;
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j) sum += acc[i][j][0] + acc[i][j][15];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
+}
+
+int run32(int blocks, int units, float* out, float* ms, double* flops) {
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1;
+  auto launch = [&]() { hipLaunchKernelGGL(probe32_kernel, dim3(blocks), dim3(512), 0, 0, out, units); };
+  launch();
+  float best = 1e30f;
+  int rc = 0;
+  for (int rep = 0; rep < 3 && rc == 0; ++rep) {
+    if (hipEventRecord(a, 0) != hipSuccess) rc = -1;
+    launch();
+    if (hipEventRecord(b, 0) != hipSuccess || hipEventSynchronize(b) != hipSuccess) rc = -1;
+    float t = 0.0f;
+    if (rc == 0 && hipEventElapsedTime(&t, a, b) != hipSuccess) rc = -1;
+    if (rc == 0 && t < best) best = t;
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *ms = best;
+  *flops = (double)blocks * 8 * units * 32.0 * 32768.0;
+  return rc == 0 && hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <int WAVES, int WAVE_COLS, bool LDS_READS, bool COPIES>
 int run(int blocks, int units, float* out, const char* src, unsigned span, int nwin, float* ms, double* flops) {
   hipEvent_t a, b;
@@ -159,7 +225,7 @@ int run(int blocks, int units, float* out, const char* src, unsigned span, int n
 
 extern "C" {
 
-// Runs probe `which` (0..3, see the top of this file) on `blocks` blocks (one
+// Runs probe `which` (0..4, see the top of this file and probe32_kernel) on `blocks` blocks (one
 // per CU) for `units` 64-deep units; out must hold blocks * 512 floats. Probe
 // 3 reads src: nwin windows of span bytes (span a power of two, at least
 // 64 KiB; units below 65536). Writes the best of three timed launches (ms) and
@@ -180,6 +246,7 @@ int pp_ceiling(int which, int blocks, int units, float* out, const void* src, un
     case 1: return run<8, 64, true, false>(blocks, units, out, s, span, nwin, ms, flops);
     case 2: return run<4, 128, true, false>(blocks, units, out, s, span, nwin, ms, flops);
     case 3: return run<8, 64, true, true>(blocks, units, out, s, span, nwin, ms, flops);
+    case 4: return run32(blocks, units, out, ms, flops);
     default: return -1;
   }
 }
