@@ -184,89 +184,6 @@ def traffic_summary(args) -> int:
     return 0
 
 
-def probe(which: str, batch: int = 16, size: int = 5120, reps: int = 3) -> int:
-    """Fixed NS (or hipBLASLt bmm) workload for rocprofv3 counter runs; prints one line per stage."""
-    import torch
-
-    from pan2_amd import _lib
-
-    dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev).manual_seed(1234)
-    if which == "bmm":
-        a = torch.randn(batch, size, size, device=dev, dtype=torch.bfloat16, generator=gen)
-        b = torch.randn(batch, size, size, device=dev, dtype=torch.bfloat16, generator=gen)
-        torch.bmm(a, b)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            torch.bmm(a, b)
-        torch.cuda.synchronize()
-        dt = (time.perf_counter() - t0) / reps
-        print(f"probe bmm {batch}x{size}^3: {dt * 1e3:.2f} ms, {2 * batch * size ** 3 / dt / 1e12:.1f} TFLOP/s")
-        return 0
-    xs = [torch.randn(size, size, device=dev, dtype=torch.bfloat16, generator=gen) for _ in range(batch)]
-    outs = [torch.empty_like(x) for x in xs]
-    _lib.newton_schulz_into(list(zip(xs, outs)))
-    torch.cuda.synchronize()
-    _lib.timing_enable(True)
-    _lib.timing_read()
-    for _ in range(reps):
-        _lib.newton_schulz_into(list(zip(xs, outs)))
-    recs = _lib.timing_read()
-    _lib.timing_enable(False)
-    for kind in ("gram", "poly", "update", "final"):
-        rs = [r for r in recs if r["kind"] == kind]
-        ms = sum(r["ms"] for r in rs)
-        print(f"probe ns {batch}x{size}^2 {kind}: {ms / reps:.2f} ms per call, "
-              f"{sum(r['flops'] for r in rs) / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
-    return 0
-
-
-def probe_ceiling(units: int = 3000) -> int:
-    """MFMA ceilings of the GEMM engine's loop on this chip (pan2_amd/csrc/pm_probe.hip):
-    MFMA alone; with the engine's LDS fragment reads and barriers (8 waves of
-    128 x 64, then 4 waves of 128 x 128); the 8-wave loop with the engine's
-    global -> LDS copies, from a 64 MiB window per XCD and from one 1 MiB window
-    that stays in L2; and MFMA alone with the 32 x 32 x 16 instruction. One
-    line each, two rounds."""
-    import ctypes
-
-    import torch
-
-    from pan2_amd.build import PROBE_LIB
-
-    dev = torch.device("cuda:0")
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    lib = ctypes.CDLL(PROBE_LIB)
-    fn = lib.pp_ceiling
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint,
-                   ctypes.c_int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_double)]
-    out = torch.empty(cus * 512, dtype=torch.float32, device=dev)
-    mib = 1 << 20
-    src = torch.empty(8 * 64 * mib // 2, dtype=torch.int16, device=dev)
-    src.random_(0, 1 << 14).bitwise_or_(0x3c00)  # bf16 in [2^-7, 2) with random mantissas, as the LDS data
-    cases = [(0, 0, 1, "mfma only (8 waves of 128x64 accumulators, register operands)"),
-             (1, 0, 1, "mfma + LDS fragment reads + 2 barriers per 64-deep unit (8 waves of 128x64)"),
-             (2, 0, 1, "mfma + LDS fragment reads + 2 barriers per 64-deep unit (4 waves of 128x128)"),
-             (3, 64 * mib, 8, "as 1 + the engine's global->LDS copies, a 64 MiB window per XCD"),
-             (3, 1 * mib, 1, "as 1 + the engine's global->LDS copies, one 1 MiB window (L2-resident)"),
-             (4, 0, 1, "mfma only with v_mfma_f32_32x32x16_bf16 (the same 128x64 accumulators as 4x2 blocks)")]
-    for _ in range(2):
-        for which, span, nwin, name in cases:
-            ms, fl = ctypes.c_float(), ctypes.c_double()
-            torch.cuda.synchronize()
-            rc = fn(which, cus, units if which != 2 else units // 2, ctypes.c_void_p(out.data_ptr()),
-                    ctypes.c_void_p(src.data_ptr()), span, nwin, ctypes.byref(ms), ctypes.byref(fl))
-            if rc != 0:
-                print(f"probe ceiling {which}: failed", file=sys.stderr)
-                return 1
-            tf = fl.value / (ms.value * 1e-3) / 1e12
-            print(f"probe ceiling {which}: {tf:.1f} TFLOP/s = {100 * tf / PEAK_BF16_TFLOPS:.1f}% of "
-                  f"{PEAK_BF16_TFLOPS} ({ms.value:.3f} ms) -- {name}", flush=True)
-    return 0
-
-
 def hbm_stream(device, mib: int = 2048, reps: int = 5) -> dict:
     """What plain streams reach on this box's HBM, beside the 8 TB/s peak the
     HBM rooflines are quoted against: torch's device copy (mib MiB read + mib
@@ -436,18 +353,9 @@ def main() -> int:
     ap.add_argument("--traffic-kernel", default="gemm", choices=sorted(TRAFFIC_KERNELS),
                     help="--traffic-summary: whose launches (gemm: the NS GEMM engine; small_update: the small-matrix "
                          "UPDATE apply)")
-    ap.add_argument("--probe", choices=("ns", "bmm", "ceiling"),
-                    help="counter probe instead of the Muon step: 'ns' runs Newton-Schulz alone on 16 x 5120^2 "
-                         "bf16 matrices through pm_newton_schulz, 'bmm' the same 16 x 5120^3 products through "
-                         "torch.bmm (hipBLASLt) for comparison; 'ceiling' the MFMA ceilings of the engine's loop "
-                         "(pan2_amd/csrc/pm_probe.hip)")
     args = ap.parse_args()
     if args.traffic_summary:
         return traffic_summary(args)
-    if args.probe == "ceiling":
-        return probe_ceiling()
-    if args.probe:
-        return probe(args.probe)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU sharding is a design, not code", file=sys.stderr)

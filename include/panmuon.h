@@ -170,7 +170,11 @@ int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp,
  * process ends, and the descriptor tables travel as kernel arguments. A
  * matrix whose own workspace exceeds the scratch fails with PM_EWORKSPACE
  * before anything is enqueued. Calls that overlap on one GPU (other threads,
- * other streams) share its scratch and race; serialise them.
+ * other streams) share its scratch and race; serialise them. The first call
+ * on a device looks the scratch up (hipGetSymbolAddress), which may load the
+ * code object: make one call outside capture before capturing a graph. A
+ * captured call enqueues kernel launches only (no memset or copy nodes); its
+ * replays re-read lr_dev on the device and step the same tensors.
  */
 #define PM_NOALLOC_SCRATCH_BYTES (256ull << 20)
 int pm_muon_step_noalloc(const pm_matrix* mats, int n, const pm_hparams* hp,

@@ -37,9 +37,6 @@ def hipcc() -> str:
     return path
 
 
-PROBE_LIB = os.path.join(HERE, "libpanprobe.so")
-
-
 def _compile(src: str, out: str, verbose: bool) -> None:
     tmp = out + ".tmp"
     cmd = [hipcc(), *HIPCC_FLAGS, src, "-o", tmp]
@@ -54,11 +51,9 @@ def _compile(src: str, out: str, verbose: bool) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile csrc/panmuon.hip into pan2_amd/libpanmuon.so (and the ceiling
-    probes of csrc/pm_probe.hip, measurement only, into libpanprobe.so);
-    returns the library's path."""
+    """Compile csrc/panmuon.hip into pan2_amd/libpanmuon.so; returns the
+    library's path."""
     _compile(os.path.join(CSRC, "panmuon.hip"), LIB, verbose)
-    _compile(os.path.join(CSRC, "pm_probe.hip"), PROBE_LIB, verbose)
     return LIB
 
 

@@ -174,9 +174,11 @@ struct Item {
 // reused once the event recorded after its copy has completed (the smallest
 // free one that holds the table, else the largest free one, regrown). The
 // pool grows while every buffer is still in flight (calls queued far behind
-// the GPU), up to kMaxStaging buffers per device; only a call made while
-// kMaxStaging uploads of its device are still queued waits, for the oldest
-// of them (the lowest sequence number).
+// the GPU), up to kMaxStaging buffers and kMaxStagingBytes of pinned memory
+// per device; a call that finds no free buffer at either limit waits for the
+// oldest upload of its device (the lowest sequence number) and reuses that
+// buffer. A device's pinned footprint is therefore at most kMaxStagingBytes,
+// or its largest single table if that is larger.
 struct Staging {
   int device;
   void* host;
@@ -185,6 +187,8 @@ struct Staging {
   uint64_t seq;  // order in which the buffer's current copy was enqueued
 };
 constexpr size_t kMaxStaging = 1024;
+constexpr size_t kMaxStagingBytes = 64ull << 20;
+constexpr size_t kStagingMin = 1 << 16;  // smallest buffer (64 KiB)
 std::mutex g_stage_mu;
 std::vector<Staging> g_stage;
 uint64_t g_stage_seq = 0;
@@ -195,17 +199,19 @@ int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_stage_mu);
   Staging* s = nullptr;
-  size_t mine = 0, oldest = SIZE_MAX;
+  size_t mine = 0, mine_bytes = 0, oldest = SIZE_MAX;
   for (size_t i = 0; i < g_stage.size(); ++i) {
     Staging& c = g_stage[i];
     if (c.device != dev) continue;
     ++mine;
+    mine_bytes += c.bytes;
     if (oldest == SIZE_MAX || c.seq < g_stage[oldest].seq) oldest = i;
     if (hipEventQuery(c.done) != hipSuccess) continue;  // its copy is still queued
     const bool fits = c.bytes >= bytes, s_fits = s && s->bytes >= bytes;
     if (!s || (fits && (!s_fits || c.bytes < s->bytes)) || (!fits && !s_fits && c.bytes > s->bytes)) s = &c;
   }
-  if (!s && mine >= kMaxStaging) {
+  const size_t want = std::max<size_t>(align_up(bytes, kStagingMin), kStagingMin);
+  if (!s && mine > 0 && (mine >= kMaxStaging || mine_bytes + want > kMaxStagingBytes)) {
     s = &g_stage[oldest];
     e = hipEventSynchronize(s->done);
     if (e != hipSuccess) return hip_fail(e, "staging event");
@@ -221,11 +227,32 @@ int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
   if (s->bytes < bytes) {
     if (s->host) {
       e = hipHostFree(s->host);  // its copy has completed
+      mine_bytes -= s->bytes;
       s->host = nullptr;
       s->bytes = 0;
       if (e != hipSuccess) return hip_fail(e, "staging free");
     }
-    const size_t want = std::max<size_t>(align_up(bytes, 1 << 16), 1 << 16);
+    // regrowing past the byte limit: release this device's other idle buffers
+    // (their copies have completed) before allocating
+    if (mine_bytes + want > kMaxStagingBytes) {
+      const uint64_t seq = s->seq;
+      for (size_t i = 0; i < g_stage.size();) {
+        Staging& c = g_stage[i];
+        if (c.device == dev && c.seq != seq && c.host && hipEventQuery(c.done) == hipSuccess) {
+          e = hipHostFree(c.host);
+          if (e != hipSuccess) return hip_fail(e, "staging free");
+          (void)hipEventDestroy(c.done);
+          g_stage[i] = g_stage.back();
+          g_stage.pop_back();
+        } else {
+          ++i;
+        }
+      }
+      s = nullptr;
+      for (Staging& c : g_stage)
+        if (c.seq == seq) s = &c;
+      if (!s) return fail(PM_EHIP, "internal: staging buffer lost");
+    }
     e = hipHostMalloc(&s->host, want, hipHostMallocDefault);
     if (e != hipSuccess) return hip_fail(e, "staging allocation");
     s->bytes = want;

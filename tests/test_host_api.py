@@ -190,3 +190,30 @@ def test_lr_scheduler_reads_base_lrs_only_at_capture(restore_torch_muon):
         sched.step()
     assert reads == [1]
     assert not any("host" in k or "pan2" in k for k in sd_keys)
+
+
+def test_lr_scheduler_base_lrs_assignment_recaptured(restore_torch_muon):
+    """Assigning a new base_lrs list (outside load_state_dict) is picked up by
+    the next get_last_lr(), with one read per base lr; an unchanged list is
+    not read again (pan/optim/patch_lr_scheduler.py:23 re-reads on list
+    identity)."""
+    from torch.optim.lr_scheduler import LambdaLR
+
+    reads = []
+
+    class Counted(float):
+        def __float__(self):
+            reads.append(1)
+            return super().__float__()
+
+    patch_lr_scheduler()
+    opt = torch.optim.SGD([torch.nn.Parameter(torch.zeros(2))], lr=0.3)
+    sched = LambdaLR(opt, lambda e: 0.5 ** e)
+    assert sched.get_last_lr() == [pytest.approx(0.3)]
+    sched.base_lrs = [Counted(0.8)]
+    assert sched.get_last_lr() == [pytest.approx(0.8)]
+    assert reads == [1]
+    opt.step()
+    sched.step()
+    assert sched.get_last_lr() == [pytest.approx(0.8 * 0.5)]
+    assert reads == [1]

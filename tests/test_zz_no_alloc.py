@@ -97,3 +97,34 @@ def test_noalloc_allocates_nothing_through_torch():
     step(state, noalloc=True, lr=0.02, ns_form="standard")
     torch.cuda.synchronize()
     assert torch.cuda.memory_stats(DEV)["allocation.all.allocated"] == before
+
+
+@pytest.mark.parametrize("ns_form", ["standard", "gram"])
+def test_noalloc_step_captured_in_a_graph_replays_the_eager_step(ns_form):
+    """pm_muon_step_noalloc captured with torch.cuda.graph after one eager call
+    (the device's first call looks up the scratch, which must not happen under
+    capture): every replay steps params and momentum to the same bits as an
+    eager workspace step on a twin state. Eager work and a synchronisation sit
+    between replays, and the device lr is changed between them (the graph reads
+    it on the device)."""
+    shapes = [(1024, 4096), (300, 1000), (96, 2000), (2000, 64), (512, 512)]
+    lr = torch.tensor(0.02, device=DEV)
+    warm = make_state(shapes, 501, torch.float32)
+    step(warm, noalloc=True, lr=lr, ns_form=ns_form)
+    torch.cuda.synchronize()
+    ref = make_state(shapes, 500, torch.float32)
+    got = make_state(shapes, 500, torch.float32)
+    graph = torch.cuda.CUDAGraph()
+    print(f"noalloc graph capture {ns_form}: {shapes}", flush=True)
+    with torch.cuda.graph(graph):
+        step(got, noalloc=True, lr=lr, ns_form=ns_form)
+    torch.cuda.synchronize()
+    for rep, lr_val in enumerate((0.02, 0.01, 0.03)):
+        lr.fill_(lr_val)
+        graph.replay()
+        step(ref, noalloc=False, lr=lr, ns_form=ns_form)
+        torch.cuda.synchronize()
+        for i in range(len(shapes)):
+            assert torch.equal(got[0][i], ref[0][i]), f"param {i} after replay {rep}"
+            assert torch.equal(got[2][i], ref[2][i]), f"momentum {i} after replay {rep}"
+    graph.reset()
