@@ -2,12 +2,12 @@
 //
 // The Muon step of one group of matrices is a fixed sequence of grouped
 // launches, each walking every matrix of the group:
-//   pm_prologue_kernel   momentum update + bf16 X/Xᵀ write + per-tile Σx²
+//   pm_prologue_kernel   momentum update + bf16 X write + per-tile Σx²
 //   pm_norm_kernel       per-matrix 1/‖X‖ and 1/‖X‖²
 //   pm_ns_gemm_kernel    x ns_steps x {GRAM, POLY, UPDATE|FINAL}
 // The GEMM kernel is one bf16 MFMA (v_mfma_f32_16x16x32_bf16) tile engine
-// with four epilogues; every operand is K-contiguous ("NT" form), which is
-// why X is kept in both orientations.
+// with four epilogues; its operands are read K-contiguous from LDS, except X
+// in C = S·X and C = Xᵀ·S, which is read transposed from LDS.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -51,10 +51,9 @@ struct MatDesc {
   float adj_ratio;    // device-lr path: adjusted_lr = lr * adj_ratio
   float neg_lr_host;  // host-lr path: -(lr * adj_ratio), rounded once
   // workspace buffers
-  // X, Xᵀ and S are in the panel layout of ws_off for large matrices,
-  // row-major for small ones (Mp = 128)
+  // X and S are in the panel layout of ws_off for large matrices; a small
+  // matrix (Mp = 128) keeps X in the layout of sm_x_off
   uint16_t* X[2];     // bf16 Mp x Np (ld Np), ping-pong
-  uint16_t* XT[2];    // bf16 Np x Mp (ld Mp), same values transposed (null for small matrices)
   // bf16 Mp x Mp work matrices. Standard form: S[0] = A = X Xᵀ,
   // S[1] = B = b A + c A². Gram form: S[0] = R, S[1] = Z, S[2] = R Z + a R,
   // S[3], S[4] = Q (ping-pong). Unused entries are null.
@@ -65,7 +64,7 @@ struct MatDesc {
   int32_t pad_;
 };
 
-// Layout of the X / Xᵀ buffers a prologue launch writes.
+// Layout of the X buffer a prologue launch writes.
 enum XLayout : int32_t {
   XL_ROW = 0,    // row-major
   XL_PANEL = 1,  // the panel layout of ws_off (large matrices)
@@ -79,7 +78,7 @@ struct ProArgs {
   int32_t mode;
   float mu;
   int32_t nesterov;
-  int32_t layout;         // of X / Xᵀ (XLayout)
+  int32_t layout;         // of X (XLayout)
   int32_t pad_;
 };
 
@@ -90,7 +89,7 @@ struct GemmArgs {
   int32_t total;          // tiles of this launch (prefix[n])
   int32_t n;
   int32_t stage;
-  int32_t cur;            // which X/XT ping-pong buffer holds the current X
+  int32_t cur;            // which X ping-pong buffer holds the current X
   int32_t first;          // iteration 0: fold the Frobenius normalisation
   int32_t mode;
   int32_t sl, sr, sd, sc;  // square-buffer operands: left, right, addend, output
@@ -105,7 +104,7 @@ struct GemmArgs {
 // ws_off, the rest row-major. The grouped Muon / Newton–Schulz path keeps all
 // of them in the panel layout; pm_gram and pm_gemm_symmetric take the caller's
 // row-major matrices.
-constexpr int kTiledX = 1;  // X and Xᵀ
+constexpr int kTiledX = 1;  // X
 constexpr int kTiledS = 2;  // the Mp x Mp work matrices
 constexpr int kWsLayout = kTiledX | kTiledS;
 

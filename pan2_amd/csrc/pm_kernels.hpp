@@ -13,14 +13,15 @@ namespace pm {
 //   MODE_STEP: buf <- mu*buf + (1-mu)*g;  u <- (1-mu)*g + mu*buf  (nesterov)
 //              (pan/optim/muon_triton.py:44-48; fp32 math)
 //   MODE_NS:   u <- in
-// X and Xᵀ get bf16(u) (torch casts to bf16 before NS, torch/optim/_muon.py:55),
-// in the layout ProArgs.layout names
+// X gets bf16(u), or bf16(uᵀ) for a tall param (torch casts to bf16 before
+// NS, torch/optim/_muon.py:55, and transposes, :56-57), in the layout
+// ProArgs.layout names
 // and partials[tile] = Σ bf16(u)², the tile's share of ‖X‖² (norm over the
 // bf16 tensor, torch/optim/_muon.py:59).
 // Each thread moves two runs of 8 consecutive elements of a row: 16-byte
 // loads and stores where the row is in range and the caller's strides and
-// bases allow, element by element otherwise. The copy in the other
-// orientation goes through an LDS tile.
+// bases allow, element by element otherwise. A transposed X goes through an
+// LDS tile.
 constexpr int kProPitch = kProTile + 8;  // LDS row pitch (elements), keeps 16-byte rows aligned
 constexpr int kProRun = 4;  // tiles per prologue block, along a tile row (1 and 2 measured slower)
 static_assert(kTile % (kProTile * kProRun) == 0, "runs tile the padded long side");
@@ -93,13 +94,13 @@ __global__ __launch_bounds__(kThreads) void pm_prologue_kernel(ProArgs args) {
   const bool step = args.mode == MODE_STEP;
   const bool gvec = vec_ok(d.grad, d.g_dt, d.g_ld);
   const bool mvec = step && vec_ok(d.mom, d.m_dt, d.m_ld);
-  // param-layout copy: the buffer whose rows follow the param rows; the other
-  // orientation goes through the LDS tile (a small matrix keeps no Xᵀ, so one
-  // of the two is absent)
-  uint16_t* dst_a = d.trans ? d.XT[0] : d.X[0];
-  const int64_t ld_a = d.trans ? d.Mp : d.Np;
-  uint16_t* dst_b = d.trans ? d.X[0] : d.XT[0];
-  const int64_t ld_b = d.trans ? d.Np : d.Mp;
+  // X = u is written in the param's orientation (dst_a); X = uᵀ (a tall
+  // param) goes through the LDS tile (dst_b). Only X is kept: the GEMM
+  // engine reads it transposed where it needs Xᵀ.
+  uint16_t* dst_a = d.trans ? nullptr : d.X[0];
+  const int64_t ld_a = d.Np;
+  uint16_t* dst_b = d.trans ? d.X[0] : nullptr;
+  const int64_t ld_b = d.Np;
   const int layout = args.layout;
   auto x_off = [&](int r, int c, int64_t ld) {
     return layout == XL_SMALL ? sm_x_off(r, c) : ws_off(r, c, ld, layout == XL_PANEL);
@@ -292,30 +293,84 @@ struct Ring {
   char* b[2];
 };
 
+// An operand is read either by rows (K-contiguous panels: X for GRAM, the
+// Mp x Mp work matrices) or transposed (TR below): the right operand of
+// C = S·X is X itself, whose rows run along N, not K. A transposed operand's unit is 64 rows (k) x 256 columns, kept in LDS
+// as 4 column blocks of 64 x 64 (8 KiB, 128-byte rows); its 32-byte chunk c
+// (16 columns) of row k is stored at chunk c ^ tsw(k). Its copy q (0..31) is
+// rows 8(q%8) .. +7 of column block q/8: in the panel layout of X (ws_off) 1 KiB
+// of consecutive memory, as for a row-read operand.
+__device__ __forceinline__ int tsw(int k) { return ((k >> 1) & 1) | (((k >> 3) & 1) << 1); }
+
 struct Engine {
   __amdgpu_buffer_rsrc_t rl, rr;
   int vl_off[2], vr_off[2];  // DMA lane offsets for even / odd loads
-  int frag[2];               // fragment lane offset for k-step 0 / 1
+  int frag[2];               // fragment lane offset for k-step 0 / 1 (row-read operands)
+  int toff[4];               // fragment lane offsets of column chunk 0..3 (transposed right operand)
   int aofs, bofs;            // this wave's first row (bytes) in an A / B unit
   int ql, qr;                // bytes from one 8-row copy of a unit to the next
   int ul, ur;                // bytes from one unit of a panel to the next
   int q0;
   bool copier;               // waves 0..3 issue every copy of the tile
+  // transposed right operand: its column blocks in the first 256-row panel of
+  // X, and the bytes from one 256-row panel to the next (the buffer resource
+  // is rebased per panel so offsets stay small for any extent)
+  const uint16_t* tbase;
+  int64_t tpanel;
 };
+
 
 __device__ __forceinline__ void dma_a(const Engine& e, char* dst, int unit, int i) {
   const int q = e.q0 + i;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(e.rl, to_lds(dst + q * 1024), 16, e.vl_off[q & 1],
                                            q * e.ql + unit * e.ul, 0, 0);
 }
+template <bool TR>
 __device__ __forceinline__ void dma_b(const Engine& e, char* dst, int unit, int i) {
   const int q = e.q0 + i;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(e.rr, to_lds(dst + q * 1024), 16, e.vr_off[q & 1],
-                                           q * e.qr + unit * e.ur, 0, 0);
+  if (TR) {
+    const __amdgpu_buffer_rsrc_t rs = panel_rsrc(
+        (const uint16_t*)((const char*)e.tbase + (int64_t)(unit >> 2) * e.tpanel), 4 * kOpBytes);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, to_lds(dst + q * 1024), 16, e.vr_off[q & 1],
+                                             (q >> 3) * kOpBytes + (unit & 3) * 8192 + (q & 7) * 1024, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(e.rr, to_lds(dst + q * 1024), 16, e.vr_off[q & 1],
+                                             q * e.qr + unit * e.ur, 0, 0);
+  }
+}
+
+// The MFMA fragment (16 rows or columns x 32 k) of a transposed operand: lane
+// 16g + i gets the operand's element (k0 + j, column c0 + i), j = 0..7, where
+// p addresses this lane's source of the first read. ds_read_b64_tr_b16 gives
+// lane 4a + b of each 16-lane group element b of the 8 bytes that lanes a,
+// a+4, a+8 and a+12 of the group address, so source lane s points at row
+// k0 + 4h + s/4, columns c0 + 4(s%4) .. +3, and the two reads (h = 0, 1, four
+// rows = 512 bytes apart) return 4 consecutive k each.
+__device__ __forceinline__ bf16x8 tr_frag(const char* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 512));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 w = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// Fragment j (16-row block of this wave's rows) of k-step s of the left
+// operand of unit buffer `buf`, and fragment j (16-column block) of the right.
+__device__ __forceinline__ bf16x8 frag_a(const Engine& e, const char* buf, int j, int s) {
+  return *(const bf16x8*)(buf + e.aofs + j * 2048 + e.frag[s]);
+}
+template <bool TR>
+__device__ __forceinline__ bf16x8 frag_b(const Engine& e, const char* buf, int j, int s) {
+  if (TR) return tr_frag(buf + e.bofs + s * 4096 + e.toff[j]);
+  return *(const bf16x8*)(buf + e.bofs + j * 2048 + e.frag[s]);
 }
 
 // Unit u in buffer S = u % 2; REL = units after this one (2 or more: steady).
-template <int S, int REL>
+// TR: the right operand is read transposed (two LDS reads a fragment instead
+// of one).
+template <int S, int REL, bool TR>
 __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine& e, f32x4 (&acc)[kMi][kNi],
                                           bf16x8 (&bf)[2][kNi], bf16x8 (&af)[8]) {
   const char* ca = ring.a[S];
@@ -334,18 +389,27 @@ __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine&
     }
     if (REL >= 1 && p == 14) {
       if (REL >= 2) wait_vmcnt<4>(); else wait_vmcnt<0>();  // A(u+1) #7 (position 1) was followed by B(u+2) #0..#3
-      wait_lgkmcnt<2>();  // the read of A(u) at position 13; only the B reads of 13 and 14 may be pending
+      // the read of A(u) at position 13 has returned: only the B read issued
+      // after it (one instruction, two if transposed) may be pending
+      wait_lgkmcnt<TR ? 2 : 1>();
       block_barrier();
     }
     if (p + 2 < 16) {
       const int q = p + 2;
-      af[q % 8] = *(const bf16x8*)(ca + e.aofs + (q % 8) * 2048 + e.frag[q / 8]);
+      af[q % 8] = frag_a(e, ca, q % 8, q / 8);
+      if (p == 13) __builtin_amdgcn_sched_barrier(0);  // the last read of A(u) stays ahead of the B read
     } else if (REL >= 1) {
       const int q = p + 2 - 16;
-      af[q % 8] = *(const bf16x8*)(na + e.aofs + q * 2048 + e.frag[0]);
+      af[q % 8] = frag_a(e, na, q, 0);
     }
-    if (p < kNi) bf[1][p] = *(const bf16x8*)(cb + e.bofs + p * 2048 + e.frag[1]);
-    if (REL >= 1 && p >= 12) bf[0][p - 12] = *(const bf16x8*)(nb + e.bofs + (p - 12) * 2048 + e.frag[0]);
+    // k-step 1's B fragments (used from position 8): one a position, two
+    // positions apart when each takes two reads
+    if (TR) {
+      if (p % 2 == 0 && p < 2 * kNi) bf[1][p / 2] = frag_b<TR>(e, cb, p / 2, 1);
+    } else if (p < kNi) {
+      bf[1][p] = frag_b<TR>(e, cb, p, 1);
+    }
+    if (REL >= 1 && p >= 12) bf[0][p - 12] = frag_b<TR>(e, nb, p - 12, 0);
 #pragma unroll
     for (int ni = 0; ni < kNi; ++ni) mfma16(acc[mi][ni], af[p % 8], bf[s][ni]);
     if (e.copier) {  // waves 0..3: two copies per position
@@ -354,8 +418,8 @@ __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine&
         dma_a(e, ring.a[S ^ 1], u + 1, 5 + 2 * p);
       }
       if (REL >= 2 && p >= 12) {
-        dma_b(e, ring.b[S], u + 2, 2 * (p - 12));
-        dma_b(e, ring.b[S], u + 2, 2 * (p - 12) + 1);
+        dma_b<TR>(e, ring.b[S], u + 2, 2 * (p - 12));
+        dma_b<TR>(e, ring.b[S], u + 2, 2 * (p - 12) + 1);
       }
       if (REL >= 2 && p >= 14) {
         dma_a(e, ring.a[S], u + 2, 2 * (p - 14));
@@ -383,13 +447,30 @@ __device__ __forceinline__ int lane_id() {
 }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// Operand panels and per-lane addressing of one tile. Panels are row-major
-// (ld elements a row) or in the panel layout of ws_off (tiled), where a unit's
-// 256 rows of 128 bytes are contiguous.
-__device__ __forceinline__ Engine make_engine(const uint16_t* __restrict__ Lp, int ldl,
-                                              const uint16_t* __restrict__ Rp, int ldr, int w, bool tl, bool tr) {
+// Operands and tile of one work item of a stage (decode_tile).
+struct TileJob {
+  const uint16_t* L;
+  const uint16_t* R;
+  int ldl, ldr, K;
+  int ti, tj;
+  bool tl, tr;  // L / R in the panel layout
+  bool rtr;     // R read transposed (X itself; needs the panel layout)
+};
+
+// Operand panels and per-lane addressing of tile (ti, tj). A row-read panel is
+// row-major (ld elements a row) or in the panel layout of ws_off (tiled),
+// where a unit's 256 rows of 128 bytes are contiguous. A transposed right
+// operand is X (panel layout, ld = Np): for tile column tj its columns
+// 256tj .. 256tj+255 are the 64-column units 4tj .. 4tj+3 of every 256-row
+// panel.
+template <bool TR>
+__device__ __forceinline__ Engine make_engine(const TileJob& j, int w) {
   const int lane = lane_id();
   Engine e;
+  const uint16_t* Lp = j.L + (int64_t)j.ti * kTile * j.ldl;
+  const uint16_t* Rp = j.R + (int64_t)j.tj * kTile * j.ldr;
+  const int ldl = j.ldl, ldr = j.ldr;
+  const bool tl = j.tl, tr = j.tr;
   e.rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
   e.rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
   const int rowl = tl ? kBK * 2 : ldl * 2, rowr = tr ? kBK * 2 : ldr * 2;  // bytes from row to row
@@ -397,13 +478,19 @@ __device__ __forceinline__ Engine make_engine(const uint16_t* __restrict__ Lp, i
   e.qr = 8 * rowr;
   e.ul = tl ? kOpBytes : kBK * 2;
   e.ur = tr ? kOpBytes : kBK * 2;
-  // DMA load q (0..31) covers rows 8q..8q+7 of a unit; copier wave w < 4 issues q = 8w..8w+7.
-  // Lane l fills row 8q + l/8 at stored chunk l%8, i.e. logical chunk (l%8) ^ ((row >> 1) & 7).
+  // Row-read copy q (0..31) covers rows 8q..8q+7 of a unit. Lane l fills row
+  // 8q + l/8 at stored chunk l%8, i.e. logical chunk (l%8) ^ ((row >> 1) & 7).
+  // Transposed copy q: lane l fills row k = 8(q%8) + l/8 of column block q/8 at
+  // stored 32-byte chunk (l%8)/2, i.e. logical chunk ((l%8)/2) ^ tsw(k), half
+  // l%2, and tsw(k) = ((l >> 4) & 1) | 2·(q % 2).
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
     const int sw = (4 * par + (lane >> 4)) & 7;
+    const int row_off = (lane >> 3) * 128;
+    const int tsw_l = ((lane >> 4) & 1) | (par << 1);
+    const int t_off = row_off + ((((((lane & 7) >> 1) ^ tsw_l) << 1) | (lane & 1)) << 4);
     e.vl_off[par] = (lane >> 3) * rowl + (((lane & 7) ^ sw) << 4);
-    e.vr_off[par] = (lane >> 3) * rowr + (((lane & 7) ^ sw) << 4);
+    e.vr_off[par] = TR ? t_off : (lane >> 3) * rowr + (((lane & 7) ^ sw) << 4);
   }
   e.q0 = w * 8;
   e.copier = w < 4;
@@ -411,8 +498,21 @@ __device__ __forceinline__ Engine make_engine(const uint16_t* __restrict__ Lp, i
   const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int s = 0; s < 2; ++s) e.frag[s] = r16 * 128 + (((4 * s + g) ^ ((r16 >> 1) & 7)) << 4);
+  // transposed fragment reads: source lane r16 of group g reads row
+  // 8g + r16/4 (+ 32 per k-step, + 4 for the second read) at columns
+  // 16c + 4(r16%4) of its block: chunk c ^ tsw(row), and tsw(row) =
+  // ((r16 >> 3) & 1) | 2·(g & 1) for every such row
+  const int tsw_f = ((r16 >> 3) & 1) | ((g & 1) << 1);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) e.toff[c] = (8 * g + (r16 >> 2)) * 128 + ((c ^ tsw_f) << 5) + 8 * (r16 & 3);
   e.aofs = (w >> 2) * kWaveRows * 128;
-  e.bofs = (w & 3) * kWaveCols * 128;
+  e.bofs = TR ? (w & 3) * 8192 : (w & 3) * kWaveCols * 128;
+  e.tbase = nullptr;
+  e.tpanel = 0;
+  if (TR) {
+    e.tbase = j.R + (int64_t)j.tj * 4 * (kOpBytes / 2);
+    e.tpanel = (int64_t)ldr * kTile * 2;
+  }
   return e;
 }
 
@@ -421,14 +521,15 @@ __device__ __forceinline__ Engine make_engine(const uint16_t* __restrict__ Lp, i
 // other four. Copier waves only. May be
 // issued while the previous tile's epilogue runs: it touches only the LDS
 // ring, which the caller has certified free with a barrier.
+template <bool TR>
 __device__ __forceinline__ void gemm_prefetch(const Engine& e, const Ring& ring) {
   if (!e.copier) return;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_b(e, ring.b[0], 0, i);
+  for (int i = 0; i < 8; ++i) dma_b<TR>(e, ring.b[0], 0, i);
 #pragma unroll
   for (int i = 0; i < 8; ++i) dma_a(e, ring.a[0], 0, i);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_b(e, ring.b[1], 1, i);
+  for (int i = 0; i < 8; ++i) dma_b<TR>(e, ring.b[1], 1, i);
 #pragma unroll
   for (int i = 0; i < 4; ++i) dma_a(e, ring.a[1], 1, i);
 }
@@ -438,6 +539,7 @@ __device__ __forceinline__ void gemm_prefetch(const Engine& e, const Ring& ring)
 // multiple of 4. Every wave waits for all its memory operations first (the
 // prefetch, and the previous tile's epilogue stores, which vmcnt also counts),
 // so the in-loop counts see only this tile's copies.
+template <bool TR>
 __device__ __forceinline__ void gemm_run(const Engine& e, int K, const Ring& ring, f32x4 (&acc)[kMi][kNi]) {
 #pragma unroll
   for (int i = 0; i < kMi; ++i)
@@ -450,9 +552,9 @@ __device__ __forceinline__ void gemm_run(const Engine& e, int K, const Ring& rin
   wait_lgkmcnt<0>();  // also publishes LDS writes made before this barrier
   block_barrier();
 #pragma unroll
-  for (int i = 0; i < kNi; ++i) bf[0][i] = *(const bf16x8*)(ring.b[0] + e.bofs + i * 2048 + e.frag[0]);
-  af[0] = *(const bf16x8*)(ring.a[0] + e.aofs + e.frag[0]);
-  af[1] = *(const bf16x8*)(ring.a[0] + e.aofs + 2048 + e.frag[0]);
+  for (int i = 0; i < kNi; ++i) bf[0][i] = frag_b<TR>(e, ring.b[0], i, 0);
+  af[0] = frag_a(e, ring.a[0], 0, 0);
+  af[1] = frag_a(e, ring.a[0], 1, 0);
   __builtin_amdgcn_sched_barrier(0);
 
   // KT >= 4, so the steady loop runs at least once; a do-while keeps a single
@@ -460,12 +562,12 @@ __device__ __forceinline__ void gemm_run(const Engine& e, int K, const Ring& rin
   const int KT = K / kBK;
   int u = 0;
   do {
-    gemm_unit<0, 2>(ring, u, e, acc, bf, af);
-    gemm_unit<1, 2>(ring, u + 1, e, acc, bf, af);
+    gemm_unit<0, 2, TR>(ring, u, e, acc, bf, af);
+    gemm_unit<1, 2, TR>(ring, u + 1, e, acc, bf, af);
     u += 2;
   } while (u < KT - 2);
-  gemm_unit<0, 1>(ring, KT - 2, e, acc, bf, af);
-  gemm_unit<1, 0>(ring, KT - 1, e, acc, bf, af);
+  gemm_unit<0, 1, TR>(ring, KT - 2, e, acc, bf, af);
+  gemm_unit<1, 0, TR>(ring, KT - 1, e, acc, bf, af);
   // The last MFMAs must have read their sources and retired before those
   // registers are reused and the accumulators read: the padding takes the
   // final accumulators and fragments as operands, so nothing that touches
@@ -502,14 +604,6 @@ __device__ __forceinline__ void for_each_quad(const f32x4 (&acc)[kMi][kNi], int 
 }
 
 
-// Operands and tile of one work item of stage STAGE.
-struct TileJob {
-  const uint16_t* L;
-  const uint16_t* R;
-  int ldl, ldr, K;
-  int ti, tj;
-  bool tl, tr;  // L / R in the panel layout
-};
 
 template <int STAGE, int LAYOUT, class D>
 __device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArgs& args) {
@@ -518,6 +612,7 @@ __device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArg
   bool sym = false;
   const int cur = args.cur;
   constexpr bool tx = LAYOUT & kTiledX, ts = LAYOUT & kTiledS;
+  j.rtr = false;
   if (STAGE == ST_GRAM) {
     j.L = j.R = d.X[cur]; j.ldl = j.ldr = d.Np; j.K = d.Np; P = Q = d.Mp; sym = true;
     j.tl = j.tr = tx;
@@ -526,28 +621,18 @@ __device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArg
     // is its own transpose)
     j.L = d.S[args.sl]; j.R = d.S[args.sr]; j.ldl = j.ldr = d.Mp; j.K = d.Mp; P = Q = d.Mp; sym = true;
     j.tl = j.tr = ts;
-  } else if (STAGE == ST_UPDATE) {
-    // C (Mp x Np) = S[sl] · X, X supplied as Xᵀ rows
-    j.L = d.S[args.sl]; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
-    j.tl = ts; j.tr = tx;
-  } else if (!d.trans) {
-    // wide FINAL: C (Np x Mp) = Xᵀ · S[sl] = (S[sl] X)ᵀ (S[sl] is symmetric), so
-    // a lane's quad (4 tile rows at one tile column) is 4 consecutive columns
-    // of one param row
-    j.L = d.XT[cur]; j.ldl = d.Mp; j.R = d.S[args.sl]; j.ldr = d.Mp; j.K = d.Mp; P = d.Np; Q = d.Mp;
-    j.tl = tx; j.tr = ts;
   } else {
-    // tall FINAL: C (Mp x Np) = S[sl] · X, whose transpose is the param: a quad
-    // is again 4 consecutive columns of one param row
-    j.L = d.S[args.sl]; j.ldl = d.Mp; j.R = d.XT[cur]; j.ldr = d.Mp; j.K = d.Mp; P = d.Mp; Q = d.Np;
-    j.tl = ts; j.tr = tx;
+    // UPDATE and FINAL: C (Mp x Np) = S[sl] · X, X read transposed. C is the
+    // param of a wide matrix and the param's transpose for a tall one.
+    j.L = d.S[args.sl]; j.ldl = d.Mp; j.R = d.X[cur]; j.ldr = d.Np; j.K = d.Mp; P = d.Mp; Q = d.Np;
+    j.tl = ts; j.tr = tx; j.rtr = true;
   }
   if (sym) {
     sym_tile(lt, P / kTile, j.ti, j.tj);
-  } else if (STAGE == ST_UPDATE) {
-    // C = S·X: the large operand is the right one (Xᵀ panels, one per tile
-    // column). Measured on bench.py --config 5: UPDATE 747.6 -> 737.1 ms per
-    // step; a tall FINAL (the same product) measured slower this way (+2.5%)
+  } else if (STAGE == ST_UPDATE || STAGE == ST_FINAL) {
+    // C = S·X: the large operand is the right one (X's column panels, one per
+    // tile column), so the XCDs walk the same few column panels at once.
+    // Measured on bench.py --config 5: UPDATE 747.6 -> 737.1 ms per step
     full_tile_cols(lt, P / kTile, Q / kTile, j.ti, j.tj);
   } else {
     full_tile(lt, P / kTile, Q / kTile, j.ti, j.tj);
@@ -736,6 +821,25 @@ __device__ __forceinline__ void unstage_quads(char* slot, const u32x4 (&raw)[2],
   }
 }
 
+// The inverse of stage_band: writes one band's full-line loads raw[2] (16
+// rows of 64 columns: lane l holds 16 bytes of row 8h + l/8 at columns
+// 8(l%8) .. +7, load_rounds' layout) to the slot in the normal staging layout
+// and reads back this lane's quads o[ni] of the band (rows 4g + r, column
+// 16 ni + lane%16): quad_transpose is its own inverse.
+__device__ __forceinline__ void unstage_band(char* slot, const u32x4 (&raw)[2], u16x4 (&o)[kNi], int lane) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 8 * h + (lane >> 3), c = lane & 7;
+    *(u32x4*)(slot + r * 128 + ((c ^ swz_norm(r)) << 4)) = raw[h];
+  }
+  const int r = 4 * (lane >> 4) + (lane & 3), c4 = (lane & 15) >> 2;
+#pragma unroll
+  for (int ni = 0; ni < kNi; ++ni) {
+    const int c = 2 * ni + (c4 >> 1);
+    o[ni] = quad_transpose(*(const u16x4*)(slot + r * 128 + ((c ^ swz_norm(r)) << 4) + ((c4 & 1) << 3)), lane);
+  }
+}
+
 // load_quads for the band group hb only (bands mi = 4hb .. 4hb+3): v[m * kNi + ni].
 __device__ __forceinline__ void load_quads_half(u16x4 (&v)[kQuads / 2], const uint16_t* __restrict__ T, int64_t ld,
                                                 bool tiled, int pbase, int qbase, int lane, int hb) {
@@ -828,10 +932,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   const int pbase = job.ti * kTile + (wave >> 2) * kWaveRows + 4 * (lane >> 4);
   const int qbase = job.tj * kTile + (wave & 3) * kWaveCols + (lane & 15);
 
-  // Epilogue operands are read as quads T[q][p0..p0+3] from the orientation
-  // whose rows run along this lane's 4 consecutive output rows p: A is
-  // symmetric, and X / Xᵀ hold the same values transposed. All loads are
-  // issued before any store, so no load waits behind stores in vmcnt order.
+  // Epilogue operands are read as full lines of rows and turned into this
+  // lane's quads (4 consecutive output rows p at one column q) through the
+  // staging slot, or as quads T[q][p0..p0+3] of a symmetric operand. All
+  // loads are issued before any store, so no load waits behind stores in
+  // vmcnt order.
   if (STAGE == ST_GRAM || STAGE == ST_SYMM) {
     uint16_t* C = d.S[args.sc];
     const int64_t ldc = d.Mp;
@@ -941,54 +1046,46 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   const float ca = args.a;
   if (STAGE == ST_UPDATE) {
     uint16_t* Xn = d.X[cur ^ 1];
-    uint16_t* XTn = d.XT[cur ^ 1];
-    const int64_t ldx = d.Np, ldxt = d.Mp;
-    // X[p][q] = Xᵀ[q][p] as full-line loads of Xᵀ (each band group's loads
-    // issued before the previous group's stores); X' and X'ᵀ go out through
-    // the staging slot
+    const int64_t ldx = d.Np;
+    // X[p][q] as full-line loads of X's rows (each band group's loads issued
+    // before the previous group's stores), turned into quads through the
+    // staging slot; X' goes out through the slot as full lines
     const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
-    u32x4 raw[kNi][2];
-    if (ca != 0.0f) load_rounds(raw, d.XT[cur], ldxt, tx, qw, pw, lane);
+    u32x4 raw[4][2];
+    if (ca != 0.0f) load_rounds(raw, d.X[cur], ldx, tx, pw, qw, lane);
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
       u16x4 o[4][kNi];
 #pragma unroll
-      for (int ni = 0; ni < kNi; ++ni) {
-        u16x4 xq[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-        if (ca != 0.0f) unstage_quads(slot, raw[ni], xq, lane);
+      for (int m = 0; m < 4; ++m) {
+        u16x4 xq[kNi] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+        if (ca != 0.0f) unstage_band(slot, raw[m], xq, lane);
+        const int mi = 4 * hb + m;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int mi = 4 * hb + m;
+        for (int ni = 0; ni < kNi; ++ni)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[m][ni][r] = f2bf((ca * bf2f(xq[m][r]) + acc[mi][ni][r]) * s);
-        }
+          for (int r = 0; r < 4; ++r) o[m][ni][r] = f2bf((ca * bf2f(xq[ni][r]) + acc[mi][ni][r]) * s);
       }
       // the second band group's X is requested before this group's stores
-      if (hb == 0 && ca != 0.0f) load_rounds(raw, d.XT[cur], ldxt, tx, qw, pw + 64, lane);
+      if (hb == 0 && ca != 0.0f) load_rounds(raw, d.X[cur], ldx, tx, pw + 64, qw, lane);
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         stage_band(slot, o[m], lane);
         const int p0 = pw + (4 * hb + m) * 16;
         stage_flush<false>(slot, lane, Xn + ws_off(p0, qw, ldx, tx), tx ? 64 : (int)ldx);
       }
-#pragma unroll
-      for (int ni = 0; ni < kNi; ++ni) {
-        const u16x4 blk[4] = {o[0][ni], o[1][ni], o[2][ni], o[3][ni]};
-        stage_block_tr(slot, blk, lane);
-        const int p0 = pw + 64 * hb;
-        stage_flush<true>(slot, lane, XTn + ws_off(qw + 16 * ni, p0, ldxt, tx), tx ? 64 : (int)ldxt);
-      }
     }
     return;
   }
 
-  // ST_FINAL: the tile is the param's transpose, so quad (p0..p0+3, q) is
-  // param row q, columns p0..p0+3, and its a·X term is T[q][p0..p0+3] with T
-  // the orientation of X whose rows are param rows. Loads and stores are
-  // 8-byte (bf16) or 16-byte (fp32) vectors where the param's row stride and
-  // base allow, else per element.
-  const uint16_t* T = d.trans ? d.XT[cur] : d.X[cur];
-  const int64_t ldt = d.trans ? d.Mp : d.Np;
+  // ST_FINAL: C = S·X (Mp x Np) holds O = bf16(s·(a·X + S X)) at element
+  // (p, q): the param's element (p, q) for a wide param, (q, p) for a tall
+  // one. The a·X term is X[p][q], read as full lines of X's rows and turned
+  // into quads through the staging slot (or element by element). Then
+  // p <- p·(1 - lr·wd) - lr·adj·O in fp32 per element.
+  const uint16_t* X = d.X[cur];
+  const int64_t ldx = d.Np;
+  const bool tall = d.trans;
   const int prow = d.rows, pcol = d.cols;
   const int64_t ldp = d.p_ld;
   float wdf = 0.0f, neg = 0.0f;
@@ -1003,24 +1100,89 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
     }
   }
   const bool step = args.mode == MODE_STEP;
+  const bool ax = !AX_IN_ACC && ca != 0.0f;
   constexpr bool f32p = PDT == DT_F32;  // MODE_NS launches the bf16 instantiation
+  // param update of 8 consecutive bf16 elements (one 16-byte run)
+  auto step8 = [&](const u32x4& on, const u32x4& pv) {
+    u32x4 out;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint16_t o2[2];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const float onv = bf2f((uint16_t)(on[k] >> (16 * half)));
+        const float pe = bf2f((uint16_t)(pv[k] >> (16 * half)));
+        o2[half] = f2bf(step ? pe * wdf + onv * neg : onv);
+      }
+      out[k] = (uint32_t)o2[0] | ((uint32_t)o2[1] << 16);
+    }
+    return out;
+  };
   if (!f32p && slot) {
-    // bf16 params: when this wave's 64 param rows x 128 columns lie inside the
-    // param and rows are 16-byte aligned, the bf16 update goes through the
-    // staging slot 16 rows x 64 columns at a time, and the param is read,
-    // stepped and written as full lines (the same fp32 operations per element)
+    // bf16 params: when this wave's 128 x 64 block lies inside the param and
+    // rows are 16-byte aligned, O goes through the staging slot and the param
+    // is read, stepped and written as full lines (the same fp32 operations
+    // per element)
     const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
-    const bool whole = qw + kWaveCols <= prow && pw + kWaveRows <= pcol && ldp % 8 == 0 &&
-                       (uintptr_t)d.param % 16 == 0;
-    if (whole) {
-      uint16_t* P = (uint16_t*)d.param;
+    const bool inside = tall ? (qw + kWaveCols <= prow && pw + kWaveRows <= pcol)
+                             : (pw + kWaveRows <= prow && qw + kWaveCols <= pcol);
+    const bool whole = inside && ldp % 8 == 0 && (uintptr_t)d.param % 16 == 0;
+    uint16_t* P = (uint16_t*)d.param;
+    if (whole && !tall) {
+      // wide: band m (16 param rows) of band group hb is staged as rows and
+      // stepped 16 rows x 64 columns at a time
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
         __builtin_amdgcn_sched_barrier(0);
-        // X (rows = param rows) as full-line loads, transposed into quads through the slot
-        const bool ax = !AX_IN_ACC && ca != 0.0f;
-        u32x4 xr[kNi][2];
-        if (ax) load_rounds(xr, T, ldt, tx, qw, pw + 64 * hb, lane);
+        u32x4 xr[4][2];
+        if (ax) load_rounds(xr, X, ldx, tx, pw + 64 * hb, qw, lane);
+        u32x4 pv[4][2];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            pv[m][h] = step ? *(const u32x4*)(P + (int64_t)(pw + 64 * hb + 16 * m + 8 * h + (lane >> 3)) * ldp + qw +
+                                              8 * (lane & 7))
+                            : (u32x4){0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          u16x4 xq[kNi] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+          if (ax) unstage_band(slot, xr[m], xq, lane);
+          u16x4 o[kNi];
+#pragma unroll
+          for (int ni = 0; ni < kNi; ++ni)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = acc[4 * hb + m][ni][e];
+              o[ni][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xq[ni][e]) + a) * s);  // bf16 update
+            }
+          stage_band(slot, o, lane);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int r = 8 * h + (lane >> 3), c = lane & 7;
+            const u32x4 on = *(const u32x4*)(slot + r * 128 + ((c ^ swz_norm(r)) << 4));
+            *(u32x4*)(P + (int64_t)(pw + 64 * hb + 16 * m + r) * ldp + qw + 8 * c) = step8(on, pv[m][h]);
+          }
+        }
+      }
+      return;
+    }
+    if (whole) {
+      // tall: the param's rows are C's columns; each 16-column block of C (16
+      // param rows) is staged transposed and stepped as full lines. The a·X
+      // quads of the band group are loaded first as 8-byte pieces of X's rows
+      // (row 4g + l%4 of a 16-row band, 4 columns) and turned by
+      // quad_transpose.
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        __builtin_amdgcn_sched_barrier(0);
+        u16x4 xb[4][kNi];
+        const int xrow = pw + 64 * hb + 4 * (lane >> 4) + (lane & 3), xcol = qw + 4 * ((lane & 15) >> 2);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int ni = 0; ni < kNi; ++ni)
+            xb[m][ni] = ax ? *(const u16x4*)(X + ws_off(xrow + 16 * m, xcol + 16 * ni, ldx, tx)) : (u16x4){0, 0, 0, 0};
         u32x4 pv[kNi][2];
 #pragma unroll
         for (int ni = 0; ni < kNi; ++ni)
@@ -1029,109 +1191,103 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
             pv[ni][h] = step ? *(const u32x4*)(P + (int64_t)(qw + 16 * ni + 8 * h + (lane >> 3)) * ldp + pw + 64 * hb +
                                                8 * (lane & 7))
                              : (u32x4){0, 0, 0, 0};
+        if (ax) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int ni = 0; ni < kNi; ++ni) xb[m][ni] = quad_transpose(xb[m][ni], lane);
+        }
 #pragma unroll
         for (int ni = 0; ni < kNi; ++ni) {
-          u16x4 xq[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-          if (ax) unstage_quads(slot, xr[ni], xq, lane);
           u16x4 blk[4];
 #pragma unroll
           for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float a = acc[4 * hb + m][ni][e];
-              blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xq[m][e]) + a) * s);  // bf16 update
+              blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xb[m][ni][e]) + a) * s);  // bf16 update
             }
           stage_block_tr(slot, blk, lane);
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int r = 8 * h + (lane >> 3), c = lane & 7;
             const u32x4 on = *(const u32x4*)(slot + r * 128 + ((c ^ swz_tr(r)) << 4));
-            u32x4 out;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              uint16_t o2[2];
-#pragma unroll
-              for (int half = 0; half < 2; ++half) {
-                const float onv = bf2f((uint16_t)(on[k] >> (16 * half)));
-                const float pe = bf2f((uint16_t)(pv[ni][h][k] >> (16 * half)));
-                o2[half] = f2bf(step ? pe * wdf + onv * neg : onv);
-              }
-              out[k] = (uint32_t)o2[0] | ((uint32_t)o2[1] << 16);
-            }
-            *(u32x4*)(P + (int64_t)(qw + 16 * ni + r) * ldp + pw + 64 * hb + 8 * c) = out;
+            *(u32x4*)(P + (int64_t)(qw + 16 * ni + r) * ldp + pw + 64 * hb + 8 * c) = step8(on, pv[ni][h]);
           }
         }
       }
       return;
     }
   }
+  // Element path (fp32 params, and tiles at a param's edge): quad by quad. A
+  // quad is 4 consecutive elements of one param row for a tall param; for a
+  // wide one it is turned across each 4-lane group (quad_transpose, every lane
+  // active) so that it is too. Loads and stores are 8-byte (bf16) or 16-byte
+  // (fp32) vectors where the param's row stride and base allow, else per
+  // element.
   const int vec_align = f32p ? 16 : 8;
   const bool vec = (ldp % 4 == 0) && ((uintptr_t)d.param % vec_align == 0);
-  // Bands of kNi quads (16 tile rows = kNi param rows x 4 columns each) are
-  // handled kBatch at a time: every load of a batch is issued before any of
-  // its results is combined, so a tile pays 8 / kBatch memory round trips.
-  // bf16 params travel as raw bf16 (2 registers a quad), fp32 as fp32 (4).
-  constexpr int kBatch = f32p ? 2 : 4;
   typedef typename PickVec<f32p>::type PV;
+  typedef typename PickVec<f32p>::elem E;
+  const int qbase_w = job.tj * kTile + (wave & 3) * kWaveCols + 4 * ((lane & 15) >> 2);  // wide: first column
 #pragma unroll
-  for (int b0 = 0; b0 < kMi; b0 += kBatch) {
+  for (int mi = 0; mi < kMi; ++mi) {
     __builtin_amdgcn_sched_barrier(0);
-    u16x4 xv[kBatch][kNi];
-    PV pv[kBatch][kNi];
 #pragma unroll
-    for (int bi = 0; bi < kBatch; ++bi)
+    for (int ni = 0; ni < kNi; ++ni) {
+      const int p0 = pbase + mi * 16, q = qbase + ni * 16;
+      u16x4 o;
 #pragma unroll
-      for (int j = 0; j < kNi; ++j) {
-        const int c0 = pbase + (b0 + bi) * 16, r = qbase + j * 16;  // param row r, columns c0..c0+3
-        xv[bi][j] = (!AX_IN_ACC && ca != 0.0f) ? *(const u16x4*)(T + ws_off(r, c0, ldt, tx)) : (u16x4){0, 0, 0, 0};
-        if (!step) continue;
-        const bool in_row = r < prow;
-        typedef typename PickVec<f32p>::elem E;
-        const E* src = (const E*)d.param + (int64_t)r * ldp + c0;
-        if (vec && in_row && c0 + 3 < pcol) {
-          pv[bi][j] = *(const PV*)src;
+      for (int e = 0; e < 4; ++e) {
+        const float x = ax ? bf2f(X[ws_off(p0 + e, q, ldx, tx)]) : 0.0f;
+        o[e] = AX_IN_ACC ? f2bf(acc[mi][ni][e] * s) : f2bf((ca * x + acc[mi][ni][e]) * s);  // bf16 update
+      }
+      // param row r, columns c0 .. c0+3
+      int r = q, c0 = p0;
+      if (!tall) {
+        o = quad_transpose(o, lane);
+        r = pbase + mi * 16 + (lane & 3);  // pbase carries the lane's 4·(lane/16)
+        c0 = qbase_w + ni * 16;
+      }
+      if (r >= prow) continue;
+      const E* src = (const E*)d.param + (int64_t)r * ldp + c0;
+      PV pv{};
+      if (step) {
+        if (vec && c0 + 3 < pcol) {
+          pv = *(const PV*)src;
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) pv[bi][j][e] = (in_row && c0 + e < pcol) ? src[e] : (E)0;
+          for (int e = 0; e < 4; ++e) pv[e] = c0 + e < pcol ? src[e] : (E)0;
         }
       }
+      float out[4];
 #pragma unroll
-    for (int bi = 0; bi < kBatch; ++bi)
-#pragma unroll
-      for (int j = 0; j < kNi; ++j) {
-        const int mi = b0 + bi;
-        const int c0 = pbase + mi * 16, r = qbase + j * 16;
-        if (r >= prow) continue;
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // bf16 orthogonalised update
-          const float on = AX_IN_ACC ? bf2f(f2bf(acc[mi][j][e] * s))
-                                     : bf2f(f2bf((ca * bf2f(xv[bi][j][e]) + acc[mi][j][e]) * s));
-          const float pe = f32p ? (float)pv[bi][j][e] : bf2f((uint16_t)pv[bi][j][e]);
-          o[e] = step ? pe * wdf + on * neg : on;
-        }
-        const bool full = vec && c0 + 3 < pcol;
-        if (f32p) {
-          float* dst = (float*)d.param + (int64_t)r * ldp + c0;
-          if (full) {
-            *(f32x4*)dst = (f32x4){o[0], o[1], o[2], o[3]};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (c0 + e < pcol) dst[e] = o[e];
-          }
+      for (int e = 0; e < 4; ++e) {
+        const float on = bf2f(o[e]);
+        const float pe = f32p ? (float)pv[e] : bf2f((uint16_t)pv[e]);
+        out[e] = step ? pe * wdf + on * neg : on;
+      }
+      const bool full = vec && c0 + 3 < pcol;
+      if (f32p) {
+        float* dst = (float*)d.param + (int64_t)r * ldp + c0;
+        if (full) {
+          *(f32x4*)dst = (f32x4){out[0], out[1], out[2], out[3]};
         } else {
-          uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
-          if (full) {
-            *(u16x4*)dst = (u16x4){f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-          } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (c0 + e < pcol) dst[e] = f2bf(o[e]);
-          }
+          for (int e = 0; e < 4; ++e)
+            if (c0 + e < pcol) dst[e] = out[e];
+        }
+      } else {
+        uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
+        if (full) {
+          *(u16x4*)dst = (u16x4){f2bf(out[0]), f2bf(out[1]), f2bf(out[2]), f2bf(out[3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (c0 + e < pcol) dst[e] = f2bf(out[e]);
         }
       }
+    }
   }
 }
 
@@ -1174,16 +1330,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   if (t < 0) return;
   int slot = 1;
 
+  // UPDATE and FINAL read their right operand, X, transposed.
+  constexpr bool kXT = STAGE == ST_UPDATE || STAGE == ST_FINAL;
+  static_assert(!kXT || (LAYOUT & kTiledX), "X read transposed needs the panel layout");
+  auto prefetch = [&](const TileJob& j) { gemm_prefetch<kXT>(make_engine<kXT>(j, wave), ring); };
   int m = find_matrix(prefix, args.n, t);
   TileJob job = decode_tile<STAGE, LAYOUT>(descs[m], t - prefix[m], args);
-  gemm_prefetch(make_engine(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl,
-                            job.R + (int64_t)job.tj * kTile * job.ldr, job.ldr, wave, job.tl, job.tr),
-                ring);
+  prefetch(job);
   for (;;) {
     f32x4 acc[kMi][kNi];
-    gemm_run(make_engine(job.L + (int64_t)job.ti * kTile * job.ldl, job.ldl,
-                         job.R + (int64_t)job.tj * kTile * job.ldr, job.ldr, wave, job.tl, job.tr),
-             job.K, ring, acc);
+    gemm_run<kXT>(make_engine<kXT>(job, wave), job.K, ring, acc);
     block_barrier();  // every wave is past its last LDS read of this tile
     const int tn = __builtin_amdgcn_readfirstlane(s_tile[slot]);
     int mn = 0;
@@ -1191,9 +1347,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     if (tn >= 0) {
       mn = find_matrix(prefix, args.n, tn);
       jn = decode_tile<STAGE, LAYOUT>(descs[mn], tn - prefix[mn], args);
-      gemm_prefetch(make_engine(jn.L + (int64_t)jn.ti * kTile * jn.ldl, jn.ldl,
-                                jn.R + (int64_t)jn.tj * kTile * jn.ldr, jn.ldr, wave, jn.tl, jn.tr),
-                    ring);
+      prefetch(jn);
     }
     const bool leader = wave == 0 && lane_id() == 0;
     int after = -1;

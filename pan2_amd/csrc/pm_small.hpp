@@ -17,8 +17,7 @@
 //                          parameter step): one persistent block per CU
 //                          streams 64-column units of X (and, for the step,
 //                          their param blocks) through an LDS ring across
-//                          matrices. Small matrices keep X only, no Xᵀ: the
-//                          apply reads X transposed from LDS.
+//                          matrices. The apply reads X transposed from LDS.
 //
 // With many matrices in a call, the R a core launch starts from is formed by
 // the kernel that wrote X instead: the UPDATE apply (its X'), and for the

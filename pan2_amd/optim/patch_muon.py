@@ -45,7 +45,7 @@ def _is_dtensor(t) -> bool:
     return isinstance(t, DTensor)
 
 
-# libpanmuon's workspace cap in bytes; 0 = the library default (32 GiB).
+# libpanmuon's workspace cap in bytes; 0 = the library default (12 GiB).
 WORKSPACE_LIMIT = 0
 
 # Newton–Schulz organisation: "standard" (torch's quintic, TORCH/optim/_muon.py:61-66)

@@ -51,6 +51,21 @@ def ns_fp32(g):
     return x.mT.contiguous() if tall else x
 
 
+def test_ns_fp32_matches_the_fp64_oracle():
+    """ns_fp32, the float32 reference the full-size and full-step tests gate
+    against, agrees with the oracle's float64 standard quintic
+    (muon_ref.ns_standard, pinned by tests/pins.py) on a wide and a tall
+    matrix, to float32 rounding; a dropped term, a transposed operand or a
+    missing normalisation would be off by O(1)."""
+    for shape in ((64, 96), (96, 64)):
+        gen = torch.Generator("cpu").manual_seed(7)
+        x = torch.randn(*shape, generator=gen, dtype=torch.float64)
+        want = muon_ref.ns_standard(x.numpy(), COEFFS, 5, 1e-7, precision="fp64")
+        got = ns_fp32(x.float().to(DEV)).double().cpu().numpy()
+        rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+        assert got.shape == want.shape and rel < 1e-5, (shape, rel)
+
+
 def singular_values(o):
     """Singular values of o (short side), from the eigenvalues of its float32 gram
     (absolute error ~1e-6 on σ², far inside the 0.03 slack)."""

@@ -11,9 +11,14 @@ config 5, BASELINE's 185 GB throughput state (small, so that the bf16 param
 still resolves the update: see below). lr 0.02, weight decay 0.01,
 momentum 0.95 Nesterov, 5 quintic steps.
 
-A sample of each config's matrices is checked (configs 2-4: every distinct
-shape; config 5: every distinct shape and every workspace group of the call):
-- momentum buffer bit-exact against oracle.muon_ref.momentum_nesterov;
+Every matrix's momentum buffer is checked bit-exactly on the device against
+momentum_dev, a float32 restatement of the momentum update in torch ops that
+test_momentum_dev_matches_the_oracle pins to oracle.muon_ref.momentum_nesterov;
+the pre-step buffer is drawn again from its seed. A sample of each config's
+matrices is checked further (configs 2-4: every distinct shape; config 5:
+every distinct shape and every workspace group of the call, the grouping
+model checked against the library's own launch records):
+- momentum buffer bit-exact against oracle.muon_ref.momentum_nesterov (CPU);
 - the update O the step applied, read back as (p0·(1 - lr·wd) - p1) / adjusted_lr,
   within relative Frobenius error 2e-2 of a float32 Newton–Schulz of the
   same momentum-blended gradient u on the GPU (the north star's gate). For
@@ -40,6 +45,7 @@ import torch
 
 import torch.optim._muon as torch_muon
 from oracle import muon_ref
+from pan2_amd import _lib
 from pan2_amd.optim.patch_muon import patch_muon
 from tests.conftest import TORCH_ZEROPOWER
 from tests.test_gpu_full_size import band, ns_fp32, singular_values
@@ -53,7 +59,7 @@ S = 5120
 BLOCK = [(S, S)] * 8 + [(4 * S, S)] * 2 + [(S, 4 * S)] * 2 + [(S, 6 * S)] * 2 + [(4096, S)]
 CONFIGS = {2: [(S, S)] * 48, 3: [(4 * S, S)] * 16 + [(S, 4 * S)] * 16, 4: BLOCK, 5: BLOCK * 24}
 QUINTIC_MAX = float(muon_ref.quintic_power(np.linspace(1e-6, 1.0, 200001)).max())  # 1.2024
-WORKSPACE_LIMIT = 32 << 30  # the library's default cap
+WORKSPACE_LIMIT = 12 << 30  # the library's default cap
 
 
 @pytest.fixture
@@ -68,14 +74,16 @@ def workspace_groups(shapes, limit=WORKSPACE_LIMIT):
     """Group index of each matrix in one pm_muon_step call: the library sorts
     by padded long side, then padded short side (both descending), and packs
     matrices in that order into groups whose workspace fits the cap (the
-    per-matrix workspace of pan2_amd/csrc/panmuon.hip's make_plan, standard form)."""
+    per-matrix workspace of pan2_amd/csrc/panmuon.hip's make_plan, standard
+    form: X twice, A and B, the prologue partials). test_full_config_step
+    checks the group sizes this model gives against the library's records."""
     def up(x, m=256):
         return (x + m - 1) // m * m
 
     plans = []
     for i, (r, c) in enumerate(shapes):
         mp, np_ = up(min(r, c)), up(max(r, c))
-        ws = 4 * up(mp * np_ * 2) + 2 * up(mp * mp * 2) + up((mp // 64) * (np_ // 64) * 4) + 256
+        ws = 2 * up(mp * np_ * 2) + 2 * up(mp * mp * 2) + up((mp // 64) * (np_ // 64) * 4) + 256
         plans.append((i, mp, np_, ws))
     order = sorted(plans, key=lambda t: (-t[2], -t[1]))
     group, used, g = {}, 0, 0
@@ -100,18 +108,60 @@ def samples(config, shapes):
     return sorted(set(pick.values()))
 
 
+def draw(i, s, p_std):
+    """Matrix i's initial (param fp32, grad bf16, momentum fp32), drawn on the GPU from seed 1234 + i."""
+    gen = torch.Generator(device=DEV).manual_seed(1234 + i)
+    p = torch.empty(s, device=DEV).normal_(0.0, p_std, generator=gen)
+    g = torch.empty(s, device=DEV).normal_(0.0, 1e-3, generator=gen).to(torch.bfloat16)
+    b = torch.empty(s, device=DEV).normal_(0.0, 1e-3, generator=gen)
+    return p, g, b
+
+
 def build(shapes, pdt, p_std):
     params, bufs = [], []
     for i, s in enumerate(shapes):
-        gen = torch.Generator(device=DEV).manual_seed(1234 + i)
-        p = torch.empty(s, device=DEV).normal_(0.0, p_std, generator=gen).to(pdt)
-        p = torch.nn.Parameter(p)
+        p0, g, b = draw(i, s, p_std)
+        p = torch.nn.Parameter(p0.to(pdt))
         if p.dtype != torch.bfloat16 and hasattr(p, "grad_dtype"):
             p.grad_dtype = None  # bf16 grads on fp32 masters (torch >= 2.10 asks for this opt-in)
-        p.grad = torch.empty(s, device=DEV).normal_(0.0, 1e-3, generator=gen).to(torch.bfloat16)
-        bufs.append(torch.empty(s, device=DEV).normal_(0.0, 1e-3, generator=gen))
+        p.grad = g
+        bufs.append(b)
         params.append(p)
     return params, bufs
+
+
+def momentum_dev(buf, grad, mu=MU):
+    """The momentum update in float32 torch ops on the device:
+    mu·buf + (1 - mu)·g, (1 - mu) itself computed in float32, each product and
+    the sum rounded separately (pan/optim/muon_triton.py:44-47)."""
+    mu32 = torch.tensor(mu, dtype=torch.float32, device=buf.device)
+    omu32 = torch.tensor(1.0, dtype=torch.float32, device=buf.device) - mu32
+    return torch.add(torch.mul(buf, mu32), torch.mul(grad.float(), omu32))
+
+
+def test_momentum_dev_matches_the_oracle():
+    """momentum_dev gives the oracle's bits (muon_ref.momentum_nesterov, fp32
+    numpy) on seeded tensors, including values whose products round
+    differently with a fused multiply-add."""
+    gen = torch.Generator("cpu").manual_seed(5)
+    b = torch.randn(257, 131, generator=gen) * 1e-3
+    g = (torch.randn(257, 131, generator=gen) * 1e-3).to(torch.bfloat16)
+    b[0, :4] = torch.tensor([1.0, -3.0e-38, 6.5e4, 0.0])
+    g[0, :4] = torch.tensor([1.0, 3.0e-38, -6.5e4, 0.0]).to(torch.bfloat16)
+    want, _ = muon_ref.momentum_nesterov(b.numpy(), g.float().numpy(), MU)
+    got = momentum_dev(b.to(DEV), g.to(DEV)).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+def check_all_momenta(config, shapes, bufs, grads, p_std):
+    """Every matrix's stepped momentum buffer against momentum_dev of its
+    pre-step buffer, drawn again from its seed (one matrix at a time)."""
+    for i, s in enumerate(shapes):
+        _, g0, b0 = draw(i, s, p_std)
+        assert torch.equal(grads[i], g0), f"config {config} matrix {i}: grad changed"
+        want = momentum_dev(b0, g0)
+        assert torch.equal(bufs[i], want), f"config {config} matrix {i}: momentum differs from momentum_dev"
+        del g0, b0, want
 
 
 def check_matrix(config, i, shape, p0, g, b0, p1, b1, adjust, pdt):
@@ -182,12 +232,29 @@ def test_full_config_step(patched, config, adjust):
     for p, b in zip(params, bufs):
         opt.state[p]["momentum_buffer"] = b
     torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    _lib.timing_read()
     t0 = time.perf_counter()
-    opt.step()
-    torch.cuda.synchronize()
+    try:
+        opt.step()
+        torch.cuda.synchronize()
+    finally:
+        launches = _lib.timing_read()
+        _lib.timing_enable(False)
     print(f"  step {1e3 * (time.perf_counter() - t0):.1f} ms (first call, includes setup)", flush=True)
+    # the library's grouping: one prologue launch per group, with its matrix count
+    lib_sizes = [r["n_matrices"] for r in launches if r["kind"] == "prologue"]
+    model = workspace_groups(shapes)
+    model_sizes = [sum(1 for g in model.values() if g == k) for k in range(max(model.values()) + 1)]
+    print(f"  workspace groups: library {lib_sizes}, model {model_sizes}", flush=True)
+    assert lib_sizes == model_sizes, "the test's grouping model disagrees with the library"
+    if config == 5:
+        assert {model[i] for i in picks} == set(range(len(model_sizes))), "a workspace group is not sampled"
     recs = []
     try:
+        check_all_momenta(config, shapes, [opt.state[p]["momentum_buffer"] for p in params],
+                          [p.grad for p in params], p_std)
+        print(f"  momentum of all {len(shapes)} matrices bit-exact", flush=True)
         for i in picks:
             p0, b0 = before[i]
             recs.append(check_matrix(config, i, shapes[i], p0, params[i].grad, b0, params[i].detach(),
