@@ -48,9 +48,11 @@ def _is_dtensor(t) -> bool:
 # libpanmuon's workspace cap in bytes; 0 = the library default (12 GiB).
 WORKSPACE_LIMIT = 0
 
-# Newton–Schulz organisation: "standard" (torch's quintic, TORCH/optim/_muon.py:61-66)
-# or "gram" (PAN 2's _gram_newtonschulz_local, pan/optim/patch_muon.py:275-334).
-NS_FORM = "standard"
+# Newton–Schulz organisation: "gram" (PAN 2's _gram_newtonschulz_local,
+# pan/optim/patch_muon.py:275-334, which PAN 2's single-tensor step calls for
+# every matrix, :164-168, and patch_muon installs, :339) or "standard" (torch's
+# quintic, TORCH/optim/_muon.py:61-66). The default is PAN 2's.
+NS_FORM = "gram"
 
 
 @torch.compiler.disable
@@ -156,8 +158,9 @@ def patch_muon(ns_form: str | None = None) -> None:
     """Install the HIP path into torch.optim._muon (pan/optim/patch_muon.py:337-339).
 
     ``ns_form`` selects the Newton–Schulz organisation for every later step:
-    "standard" (torch's quintic) or "gram" (the reference's production
-    _gram_newtonschulz_local); None keeps the current choice (``NS_FORM``).
+    "gram" (the reference's production _gram_newtonschulz_local, the default)
+    or "standard" (torch's quintic); None keeps the current choice
+    (``NS_FORM``).
     Loads libpanmuon first, so a missing or broken build fails here, loudly.
     """
     global NS_FORM

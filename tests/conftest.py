@@ -80,3 +80,14 @@ def torch_fused_adam():
             _torch_adam._fused_adam = saved
 
     return stock
+
+
+@pytest.fixture(autouse=True)
+def _restore_patch_muon_switches():
+    """Restores the drop-in's module switches (NS_FORM, WORKSPACE_LIMIT) after
+    every test, whatever the test set them to."""
+    import pan2_amd.optim.patch_muon as pm
+
+    saved = (pm.NS_FORM, pm.WORKSPACE_LIMIT)
+    yield
+    pm.NS_FORM, pm.WORKSPACE_LIMIT = saved

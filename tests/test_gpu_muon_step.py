@@ -27,10 +27,14 @@ DEV = torch.device("cuda:0")
 
 @pytest.fixture
 def patched():
-    saved = (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon)
-    patch_muon()
+    """The HIP path with the standard quintic, whose gates these tests check
+    (the gram form, the drop-in's default, has its own in test_gpu_gram_form)."""
+    import pan2_amd.optim.patch_muon as pm
+
+    saved = (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, pm.NS_FORM)
+    patch_muon(ns_form="standard")
     yield
-    torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon = saved
+    torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon, pm.NS_FORM = saved
 
 
 def cpu_rand(shape, seed, std):
@@ -189,6 +193,7 @@ def test_factory_tensor_lr_installs_hip_path():
         import pan2_amd.optim.patch_muon as pm
 
         assert torch_muon._single_tensor_muon is pm._single_tensor_muon
+        assert pm.NS_FORM == "gram", "the drop-in installs the reference's gram-form NS by default"
         x = torch.randn(8, 256, device=DEV)
         model(x).square().sum().backward()
         w0 = model[0].weight.detach().clone()
