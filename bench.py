@@ -282,27 +282,6 @@ def bench_adamw(args) -> int:
     kern_ms = sum(r["ms"] for r in recs) / max(1, len(recs))
     achieved = bytes_per_step / (kern_ms * 1e-3) / 1e9 if kern_ms > 0 else 0.0
     stream = hbm_stream(device)
-    # The reference's production organisation (gram form) on the same state,
-    # after the headline timing: its own executed FLOPs over its step time.
-    gram_form = None
-    if args.ns_form == "standard" and not args.no_gram_form and not args.copy_mib:
-        patch_muon(ns_form="gram")
-        for _ in range(max(1, args.warmup)):
-            opt.step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            opt.step()
-        torch.cuda.synchronize()
-        g_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        f_gf = sum(gram_form_flops(s) for s in units)
-        gram_form = {"ms_per_step": round(g_ms, 3), "f_gram_form": f_gf,
-                     "executed_tflops": round(f_gf / (g_ms * 1e-3) / 1e12, 1),
-                     "pct_peak_executed": round(100 * f_gf / (g_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
-                     "steps": args.steps}
-        print(f"bench: gram form {g_ms:.2f} ms/step", file=sys.stderr, flush=True)
-        patch_muon(ns_form=args.ns_form)
-
     cpu = None
     if not args.no_cpu_baseline:
         # torch's CPU AdamW (foreach) over the same set, one timed step after one warmup
