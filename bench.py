@@ -127,10 +127,12 @@ def traffic_path(workload: str, kernel: str = "gemm") -> str:
     return os.path.join(ROOT, "profiles", f"{TRAFFIC_KERNELS[kernel][1]}_{workload}_traffic.json")
 
 
-def traffic_bytes(workload: str, kernel: str = "gemm"):
-    """HBM bytes per launch of the kernel from the committed counter summary, or None."""
+def traffic_bytes(workload: str, kernel: str = "gemm", ns_form: str = "standard"):
+    """HBM bytes per launch of the kernel from the committed counter summary,
+    or None. The summaries are measured on the standard form (the default
+    bench command), so a gram-form line reports None."""
     path = traffic_path(workload, kernel)
-    if not os.path.exists(path):
+    if ns_form != "standard" or not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f)["bytes_per_launch"]
@@ -448,7 +450,7 @@ def main() -> int:
         gbs = up_bytes / (up_ms * 1e-3) / 1e9 if up_ms > 0 else 0.0
         roofline = {"kernel": "pm_small_apply_kernel<UPDATE>", "bound": "hbm", "achieved": round(gbs, 1),
                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                    "traffic": traffic_bytes(name, "small_update"), "bytes_per_element": 4, "launches": len(ups),
+                    "traffic": traffic_bytes(name, "small_update", args.ns_form), "bytes_per_element": 4, "launches": len(ups),
                     "avg_launch_ms": round(up_ms / max(1, len(ups)), 3)}
     else:
         roofline = {
@@ -458,7 +460,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": traffic_bytes(name),
+            "traffic": traffic_bytes(name, ns_form=args.ns_form),
             "launches": len(gemm),
             "avg_launch_ms": round(gemm_ms / max(1, len(gemm)), 3),
         }
