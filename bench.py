@@ -434,7 +434,8 @@ def main() -> int:
     f_run = f_ns if args.ns_form == "standard" else sum(gram_form_flops(s) for s in units)
     value = f_run / (ms_per_step * 1e-3) / 1e12
 
-    gemm = [r for r in recs if r["kind"] in ("gram", "poly", "update", "final")]
+    # the GEMM engine's launches, K-split reduces included (their epilogues are the stage's)
+    gemm = [r for r in recs if r["kind"] in ("gram", "poly", "update", "final", "reduce")]
     gemm_ms = sum(r["ms"] for r in gemm)
     gemm_flops = sum(r["flops"] for r in gemm)
     achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
@@ -465,7 +466,7 @@ def main() -> int:
             "avg_launch_ms": round(gemm_ms / max(1, len(gemm)), 3),
         }
     stages = {}
-    for kind in ("prologue", "norm", "gram", "poly", "qinit", "small_core", "update", "final"):
+    for kind in ("prologue", "norm", "gram", "poly", "qinit", "small_core", "update", "final", "reduce"):
         rs = [r for r in recs if r["kind"] == kind]
         if not rs:
             continue

@@ -298,7 +298,7 @@ int pm_adam_step(const pm_adam_tensor* tensors, int n, const pm_adam_hparams* hp
  * per launch with its algorithmic work.
  */
 enum pm_kernel_kind {
-  PM_K_PROLOGUE = 0,  /* momentum + bf16 X/Xᵀ + Σx² partials */
+  PM_K_PROLOGUE = 0,  /* momentum + bf16 X + Σx² partials */
   PM_K_NORM = 1,      /* per-matrix 1/‖X‖ */
   PM_K_GRAM = 2,      /* A = X Xᵀ (symmetric) */
   PM_K_POLY = 3,      /* symmetric product: B = b A + c A² (standard form);
@@ -309,7 +309,11 @@ enum pm_kernel_kind {
   PM_K_SMALL_CORE = 7, /* matrices with min(rows, cols) <= 128: gram and the
                          M x M part of one iteration (standard form) or of one
                          segment (gram form), in one launch */
-  PM_K_ADAM = 8        /* pm_adam_step: step counts and the element update */
+  PM_K_ADAM = 8,       /* pm_adam_step: step counts and the element update */
+  PM_K_REDUCE = 9      /* a K-split stage's second launch: the chunks' fp32
+                         partial tiles summed in chunk order, then the stage's
+                         epilogue (matrices of 512 <= Mp whose own tiles leave
+                         most of the chip idle; flops 0, counted by the stage) */
 };
 
 typedef struct pm_launch_time {

@@ -53,7 +53,7 @@ EXPORTS = (
     "pm_adam_step",
 )
 
-KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit", "small_core", "adam")
+KERNEL_KINDS = ("prologue", "norm", "gram", "poly", "update", "final", "qinit", "small_core", "adam", "reduce")
 
 
 class PmMatrix(ctypes.Structure):

@@ -64,6 +64,8 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 struct Plan {
   int32_t rows, cols, trans, M, N, Mp, Np;
   bool small;
+  int32_t ks_gram, ks_symm, ks_full;  // K-split chunks per tile (k_split), 1: unsplit
+  size_t kpart;                       // bytes of fp32 partial tiles (the largest split stage's)
   size_t ws;  // workspace bytes of this matrix
   double flops;
 };
@@ -86,8 +88,20 @@ Plan make_plan(int64_t rows, int64_t cols, int form) {
   const size_t x = align_up((size_t)p.Mp * p.Np * 2);
   const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
   const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);  // (covers every run count)
-  // X ping-pong, the square work matrices, the prologue partials
-  p.ws = 2 * x + (size_t)square_bufs(form, p.small) * a + part + kAlign;
+  // K-split of each GEMM stage (engine matrices only): GRAM contracts over Np,
+  // the symmetric products and UPDATE / FINAL over Mp
+  const int32_t nt = p.Mp / kTile, sym = nt * (nt + 1) / 2, full = nt * (p.Np / kTile);
+  p.ks_gram = p.small ? 1 : k_split(p.Mp, sym, p.Np / 64);
+  p.ks_symm = p.small ? 1 : k_split(p.Mp, sym, p.Mp / 64);
+  p.ks_full = p.small ? 1 : k_split(p.Mp, full, p.Mp / 64);
+  size_t kp = 0;
+  const size_t tile_bytes = (size_t)kTile * kTile * 4;
+  if (p.ks_gram > 1) kp = std::max(kp, (size_t)sym * p.ks_gram * tile_bytes);
+  if (p.ks_symm > 1) kp = std::max(kp, (size_t)sym * p.ks_symm * tile_bytes);
+  if (p.ks_full > 1) kp = std::max(kp, (size_t)full * p.ks_full * tile_bytes);
+  p.kpart = kp;
+  // X ping-pong, the square work matrices, the prologue partials, the K-split partials
+  p.ws = 2 * x + (size_t)square_bufs(form, p.small) * a + part + kAlign + kp;
   const double M = p.M, N = p.N;
   p.flops = M * (M + 1) * N + M * M * (M + 1) + 2 * M * M * N;
   return p;
@@ -101,17 +115,21 @@ int gram_reset(int steps) { return steps > 2 ? 2 : -1; }
 // GRAM, POLY and UPDATE/FINAL per iteration; gram = two grams, at most four
 // symmetric products per iteration, the apply at the reset and FINAL.
 int gemm_launches(const pm_hparams* hp) {
-  return hp->ns_form == NS_GRAM ? 4 * hp->ns_steps + 4 : 3 * hp->ns_steps;
+  // x2: a stage over both unsplit and K-split matrices is two GEMM launches
+  return 2 * (hp->ns_form == NS_GRAM ? 4 * hp->ns_steps + 4 : 3 * hp->ns_steps);
 }
 
 // Descriptor table layout:
-//   descs[n] | pro_prefix[n+1] | sym_prefix[n+1] | full_prefix[n+1] | queues[launches][kXcds] | coeffs
+//   descs[n] | pro_prefix[n+1] | per stage (GRAM, symmetric products, UPDATE / FINAL) three prefix sums
+//   [n+1]: tiles of unsplit matrices, work items (tiles x K-split chunks) of split ones, tiles of split
+//   ones (the reduce launch) | queues[launches][kXcds] | coeffs
 // The queue counters are uploaded as zeros with the rest of the table, so
 // every GEMM launch starts with empty counters without a memset. coeffs holds
 // the (a, b, c) of every iteration, which the small-matrix core launch reads.
 constexpr int kMaxSteps = 99;
 constexpr size_t kCoeffBytes = (3 * kMaxSteps * 4 + kAlign - 1) / kAlign * kAlign;
-size_t queue_offset(int n) { return align_up((size_t)n * sizeof(MatDesc)) + 3 * align_up((size_t)(n + 1) * 4); }
+constexpr int kPrefixArrays = 10;
+size_t queue_offset(int n) { return align_up((size_t)n * sizeof(MatDesc)) + kPrefixArrays * align_up((size_t)(n + 1) * 4); }
 size_t coeff_offset(int n, int launches) { return queue_offset(n) + align_up((size_t)launches * kXcds * 4); }
 size_t table_bytes(int n, int launches) { return coeff_offset(n, launches) + kCoeffBytes; }
 
@@ -343,9 +361,15 @@ void timing_mark(hipStream_t stream, int kind, int group, int iteration, int nma
 // all matrices of the group and takes the next set of queue counters.
 struct Launcher {
   GemmArgs ga;          // shared fields (descs, n, mode, lr, wd) already set
-  const int32_t* sym;   // device prefix sums: symmetric (upper-triangle) tiles
-  const int32_t* full;  // device prefix sums: full tiles
-  int32_t sym_total, full_total, sym_grid, full_grid;
+  // One stage's device prefix sums: work items (tiles x K-split chunks) of the
+  // GEMM launch, and split tiles of the reduce launch that follows it
+  struct Stage {
+    const int32_t* tiles;   // unsplit matrices' tiles
+    const int32_t* items;   // split matrices' work items (tiles x chunks)
+    const int32_t* split;   // split matrices' tiles
+    int32_t tiles_total, items_total, split_total;
+  };
+  Stage gram_s, sym_s, full_s;
   int32_t* queues;      // kXcds counters per GEMM launch, zero at upload
   int launch = 0, max_launches = 0;
   bool final_f32 = false;
@@ -358,39 +382,60 @@ struct Launcher {
     a.queues = queues + kXcds * launch++;
     return PM_OK;
   }
+  // The GEMM launch of one stage over the group's work items, then, when some
+  // matrix splits this stage, the reduce launch over its split tiles.
+  // The launches of one stage: the GEMM over unsplit matrices' tiles; then,
+  // when some matrix splits this stage, the GEMM over their chunk items
+  // (fp32 partials) and the reduce over their tiles. The stage's FLOPs go
+  // with its first launch.
+  template <int STAGE, int PDT>
+  int stage_launch(GemmArgs a, const Stage& st, int kind, int it, double flops, const char* what) {
+    if (st.tiles_total > 0) {
+      a.prefix = st.tiles;
+      a.total = st.tiles_total;
+      if (int rc = next_queues(a)) return rc;
+      hipLaunchKernelGGL((pm_ns_gemm_kernel<STAGE, PDT, kWsLayout>), dim3(gemm_grid(st.tiles_total)),
+                         dim3(kGemmThreads), 0, stream, a);
+      timing_mark(stream, kind, group, it, count, flops, 0.0);
+      flops = 0.0;
+      if (int rc = check(what)) return rc;
+    }
+    if (st.items_total == 0) return PM_OK;
+    a.prefix = st.items;
+    a.total = st.items_total;
+    if (int rc = next_queues(a)) return rc;
+    hipLaunchKernelGGL((pm_ns_gemm_kernel<STAGE, PDT, kWsLayout, true>), dim3(gemm_grid(st.items_total)),
+                       dim3(kGemmThreads), 0, stream, a);
+    timing_mark(stream, kind, group, it, count, flops, 0.0);
+    if (int rc = check(what)) return rc;
+    a.prefix = st.split;
+    a.total = st.split_total;
+    a.queues = nullptr;
+    // one single-wave block per (split tile, 128 x 64 sub-tile)
+    hipLaunchKernelGGL((pm_ns_reduce_kernel<STAGE, PDT, kWsLayout>), dim3(st.split_total * (kGemmThreads / 64)),
+                       dim3(64), 0, stream, a);
+    timing_mark(stream, PM_K_REDUCE, group, it, count, 0.0, 0.0);
+    return check("K-split reduce launch");
+  }
   int gram(int cur, bool first, int sc, int it) {
     GemmArgs a = ga;
     a.stage = ST_GRAM; a.cur = cur; a.first = first; a.sc = sc;
-    a.prefix = sym; a.total = sym_total;
-    if (int rc = next_queues(a)) return rc;
-    hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_GRAM, DT_BF16, kWsLayout>), dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
-    timing_mark(stream, PM_K_GRAM, group, it, count, f_gram, 0.0);
-    return check("gram launch");
+    return stage_launch<ST_GRAM, DT_BF16>(a, gram_s, PM_K_GRAM, it, f_gram, "gram launch");
   }
   // S[sc] = alpha·S[sl]·S[sr]ᵀ + beta·S[sd]
   int symm(int sl, int sr, int sd, int sc, float alpha, float beta, int it) {
     GemmArgs a = ga;
     a.stage = ST_SYMM; a.sl = sl; a.sr = sr; a.sd = sd; a.sc = sc; a.c = alpha; a.b = beta;
-    a.prefix = sym; a.total = sym_total;
-    if (int rc = next_queues(a)) return rc;
-    hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_SYMM, DT_BF16, kWsLayout>), dim3(sym_grid), dim3(kGemmThreads), 0, stream, a);
-    timing_mark(stream, PM_K_POLY, group, it, count, f_sym, 0.0);
-    return check("symmetric product launch");
+    return stage_launch<ST_SYMM, DT_BF16>(a, sym_s, PM_K_POLY, it, f_sym, "symmetric product launch");
   }
   // X' = s·(a·X + S[sl]·X) into the other X slot, or (last) the param step
   int update(int sl, float coef_a, int cur, bool first, bool last, int it) {
     GemmArgs a = ga;
     a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = sl; a.a = coef_a; a.cur = cur; a.first = first;
-    a.prefix = full; a.total = full_total;
-    if (int rc = next_queues(a)) return rc;
-    if (last && final_f32)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_F32, kWsLayout>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
-    else if (last)
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_FINAL, DT_BF16, kWsLayout>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((pm_ns_gemm_kernel<ST_UPDATE, DT_BF16, kWsLayout>), dim3(full_grid), dim3(kGemmThreads), 0, stream, a);
-    timing_mark(stream, last ? PM_K_FINAL : PM_K_UPDATE, group, it, count, f_upd, 0.0);
-    return check("Newton-Schulz update launch");
+    const char* what = "Newton-Schulz update launch";
+    if (last && final_f32) return stage_launch<ST_FINAL, DT_F32>(a, full_s, PM_K_FINAL, it, f_upd, what);
+    if (last) return stage_launch<ST_FINAL, DT_BF16>(a, full_s, PM_K_FINAL, it, f_upd, what);
+    return stage_launch<ST_UPDATE, DT_BF16>(a, full_s, PM_K_UPDATE, it, f_upd, what);
   }
   // small matrices: R = X Xᵀ (or, r_in, the R an apply left in S[0]) and the
   // M x M part of `steps` iterations from it0 (steps == 0: the standard form's
@@ -411,8 +456,8 @@ struct Launcher {
   int small_apply(float coef_a, int cur, bool first, bool last, int it, bool gram = false) {
     GemmArgs a = ga;
     a.stage = last ? ST_FINAL : ST_UPDATE; a.sl = 0; a.sc = 0; a.a = coef_a; a.cur = cur; a.first = first;
-    a.prefix = full; a.total = full_total;
-    const dim3 grid(full_grid), block(kSmApplyThreads);  // persistent: one block per CU
+    a.prefix = full_s.tiles; a.total = full_s.tiles_total;
+    const dim3 grid(gemm_grid(full_s.tiles_total)), block(kSmApplyThreads);  // persistent: one block per CU
     if (last && final_f32)
       hipLaunchKernelGGL((pm_small_apply_kernel<ST_FINAL, DT_F32>), grid, block, 0, stream, a);
     else if (last)
@@ -564,10 +609,13 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   char* cursor = ws + tb;
   std::vector<char> host(tb, 0);
   MatDesc* descs = (MatDesc*)host.data();
+  const size_t pstride = align_up((size_t)(count + 1) * 4);
   int32_t* pro = (int32_t*)(host.data() + align_up((size_t)count * sizeof(MatDesc)));
-  int32_t* sym = (int32_t*)((char*)pro + align_up((size_t)(count + 1) * 4));
-  int32_t* full = (int32_t*)((char*)sym + align_up((size_t)(count + 1) * 4));
-  const int32_t* queues = (const int32_t*)((char*)full + align_up((size_t)(count + 1) * 4));  // zeros
+  // per stage: [0] tiles of unsplit matrices, [1] items of split ones, [2] tiles of split ones
+  int32_t* pre[3][3];
+  for (int st = 0; st < 3; ++st)
+    for (int k = 0; k < 3; ++k) pre[st][k] = (int32_t*)((char*)pro + (1 + 3 * st + k) * pstride);
+  const int32_t* queues = (const int32_t*)(host.data() + queue_offset(count));  // zeros
   float* coeffs = (float*)(host.data() + coeff_offset(count, gemm_launches(hp)));
   const Coeffs co{hp};
   for (int it = 0; it < hp->ns_steps; ++it) {
@@ -576,7 +624,9 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     coeffs[3 * it + 1] = k.b;
     coeffs[3 * it + 2] = k.c;
   }
-  pro[0] = sym[0] = full[0] = 0;
+  pro[0] = 0;
+  for (auto& st : pre)
+    for (int32_t* a : st) a[0] = 0;
   int max_mp = 0;
   for (int i = 0; i < count; ++i) {
     Item& it = items[i];
@@ -595,10 +645,19 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
     d.partials = (float*)cursor; cursor += align_up((size_t)pro_tiles(p) * 4);
     d.scales = (float*)cursor; cursor += kAlign;
     d.pro_tiles = pro_tiles(p);
+    d.ks_gram = p.ks_gram; d.ks_symm = p.ks_symm; d.ks_full = p.ks_full;
+    d.kpart = p.kpart ? (float*)cursor : nullptr;
+    cursor += p.kpart;
     descs[i] = d;
     pro[i + 1] = pro[i] + pro_tiles(p);
-    sym[i + 1] = sym[i] + sym_tiles(p);
-    full[i + 1] = full[i] + full_tiles(p);
+    const int32_t tiles[3] = {sym_tiles(p), sym_tiles(p), full_tiles(p)};
+    const int32_t ks[3] = {p.ks_gram, p.ks_symm, p.ks_full};
+    for (int st = 0; st < 3; ++st) {
+      const bool split = ks[st] > 1;
+      pre[st][0][i + 1] = pre[st][0][i] + (split ? 0 : tiles[st]);
+      pre[st][1][i + 1] = pre[st][1][i] + (split ? tiles[st] * ks[st] : 0);
+      pre[st][2][i + 1] = pre[st][2][i] + (split ? tiles[st] : 0);
+    }
     max_mp = std::max(max_mp, p.Mp);
   }
   int rc = path == TablePath::kStaged ? upload(host.data(), tb, ws, stream)
@@ -622,8 +681,7 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
 
   const MatDesc* ddesc = (const MatDesc*)ws;
   const int32_t* dpro = (const int32_t*)(ws + ((char*)pro - host.data()));
-  const int32_t* dsym = (const int32_t*)(ws + ((char*)sym - host.data()));
-  const int32_t* dfull = (const int32_t*)(ws + ((char*)full - host.data()));
+  auto dev_ptr = [&](const int32_t* h) { return (const int32_t*)(ws + ((const char*)h - host.data())); };
   int32_t* dqueues = (int32_t*)(ws + ((const char*)queues - host.data()));
 
   // Small matrices: with many of them the apply takes the fused gram (one
@@ -634,11 +692,12 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   if (small) {
     int32_t longest = 0, parts = 0;
     for (int i = 0; i < count; ++i) {
-      longest = std::max(longest, full[i + 1] - full[i]);
+      longest = std::max(longest, pre[2][0][i + 1] - pre[2][0][i]);
       parts = std::max(parts, pro[i + 1] - pro[i]);
     }
-    const int grid = gemm_grid(full[count]);
-    fused = count >= grid && (int64_t)longest * grid <= 2 * (int64_t)full[count];
+    const int32_t units = pre[2][0][count];  // small matrices never split
+    const int grid = gemm_grid(units);
+    fused = count >= grid && (int64_t)longest * grid <= 2 * (int64_t)units;
     pro_gram = fused && parts <= kSmProParts;
   }
 
@@ -673,12 +732,10 @@ int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode,
   L.ga.lr_dev = lr_dev;
   L.ga.wd = (float)hp->weight_decay;
   L.ga.wdf_host = (float)(1.0 - lr_host * (double)hp->weight_decay);
-  L.sym = dsym;
-  L.full = dfull;
-  L.sym_total = sym[count];
-  L.full_total = full[count];
-  L.sym_grid = gemm_grid(sym[count]);
-  L.full_grid = gemm_grid(full[count]);
+  Launcher::Stage* sts[3] = {&L.gram_s, &L.sym_s, &L.full_s};
+  for (int st = 0; st < 3; ++st)
+    *sts[st] = Launcher::Stage{dev_ptr(pre[st][0]), dev_ptr(pre[st][1]), dev_ptr(pre[st][2]), pre[st][0][count],
+                               pre[st][1][count], pre[st][2][count]};
   L.queues = dqueues;
   L.max_launches = gemm_launches(hp);
   L.final_f32 = mode == MODE_STEP && items[0].desc.p_dt == PM_DTYPE_F32;

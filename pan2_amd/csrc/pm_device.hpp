@@ -61,7 +61,11 @@ struct MatDesc {
   float* partials;    // Σx² of each prologue tile
   float* scales;      // [0] = 1/max(‖X‖,eps)², [1] = 1/max(‖X‖,eps)
   int32_t pro_tiles;
+  // K-split chunks per tile (k_split) of GRAM, of the symmetric products and
+  // of UPDATE / FINAL; 0 or 1: unsplit
+  int32_t ks_gram, ks_symm, ks_full;
   int32_t pad_;
+  float* kpart;       // fp32 partial tiles of split stages (chunk-major), or null
 };
 
 // Layout of the X buffer a prologue launch writes.

@@ -451,10 +451,11 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 struct TileJob {
   const uint16_t* L;
   const uint16_t* R;
-  int ldl, ldr, K;
+  int ldl, ldr, K;   // K: the item's share of the contraction (a chunk's, when split)
   int ti, tj;
   bool tl, tr;  // L / R in the panel layout
   bool rtr;     // R read transposed (X itself; needs the panel layout)
+  int u0;       // first unit (64 k) of the item's K range: a K-split chunk's offset
 };
 
 // Operand panels and per-lane addressing of tile (ti, tj). A row-read panel is
@@ -467,12 +468,16 @@ template <bool TR>
 __device__ __forceinline__ Engine make_engine(const TileJob& j, int w) {
   const int lane = lane_id();
   Engine e;
-  const uint16_t* Lp = j.L + (int64_t)j.ti * kTile * j.ldl;
-  const uint16_t* Rp = j.R + (int64_t)j.tj * kTile * j.ldr;
   const int ldl = j.ldl, ldr = j.ldr;
   const bool tl = j.tl, tr = j.tr;
-  e.rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2);
-  e.rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2);
+  // a K-split chunk starts u0 units into the panels: its bases move there
+  // (a unit is 32 KiB of a panel-layout panel, 128 bytes of a row-major row)
+  const uint32_t lskip = (uint32_t)j.u0 * (tl ? kOpBytes : kBK * 2);
+  const uint32_t rskip = (uint32_t)j.u0 * (tr ? kOpBytes : kBK * 2);
+  const uint16_t* Lp = j.L + (int64_t)j.ti * kTile * j.ldl + lskip / 2;
+  const uint16_t* Rp = j.R + (int64_t)j.tj * kTile * j.ldr + rskip / 2;
+  e.rl = panel_rsrc(Lp, (uint32_t)kTile * ldl * 2 - lskip);
+  e.rr = panel_rsrc(Rp, (uint32_t)kTile * ldr * 2 - rskip);
   const int rowl = tl ? kBK * 2 : ldl * 2, rowr = tr ? kBK * 2 : ldr * 2;  // bytes from row to row
   e.ql = 8 * rowl;
   e.qr = 8 * rowr;
@@ -510,8 +515,10 @@ __device__ __forceinline__ Engine make_engine(const TileJob& j, int w) {
   e.tbase = nullptr;
   e.tpanel = 0;
   if (TR) {
-    e.tbase = j.R + (int64_t)j.tj * 4 * (kOpBytes / 2);
+    // X read transposed: unit u is 64 rows of X, so u0 (a multiple of 4)
+    // skips u0/4 whole 256-row panels
     e.tpanel = (int64_t)ldr * kTile * 2;
+    e.tbase = j.R + (int64_t)j.tj * 4 * (kOpBytes / 2) + (int64_t)(j.u0 >> 2) * (e.tpanel / 2);
   }
   return e;
 }
@@ -605,7 +612,20 @@ __device__ __forceinline__ void for_each_quad(const f32x4 (&acc)[kMi][kNi], int 
 
 
 
-template <int STAGE, int LAYOUT, class D>
+// Tiles of one matrix in a stage (upper triangle for the symmetric ones) and
+// the stage's K-split chunks per tile (1: unsplit).
+template <int STAGE, class D>
+__device__ __forceinline__ int stage_tiles(const D& d) {
+  const int nt = d.Mp / kTile;
+  return (STAGE == ST_GRAM || STAGE == ST_SYMM) ? nt * (nt + 1) / 2 : nt * (d.Np / kTile);
+}
+template <int STAGE, class D>
+__device__ __forceinline__ int stage_split(const D& d) {
+  const int ks = STAGE == ST_GRAM ? d.ks_gram : STAGE == ST_SYMM ? d.ks_symm : d.ks_full;
+  return ks > 1 ? ks : 1;
+}
+
+template <int STAGE, int LAYOUT, bool SPLIT = false, class D>
 __device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArgs& args) {
   TileJob j;
   int P, Q;
@@ -626,6 +646,16 @@ __device__ __forceinline__ TileJob decode_tile(const D& d, int lt, const GemmArg
     // param of a wide matrix and the param's transpose for a tall one.
     j.L = d.S[args.sl]; j.ldl = d.Mp; j.R = d.X[cur]; j.ldr = d.Np; j.K = d.Mp; P = d.Mp; Q = d.Np;
     j.tl = ts; j.tr = tx; j.rtr = true;
+  }
+  // SPLIT: work item lt is chunk `chunk` of tile `tile` (chunk-major), its K
+  // range the chunk's share of the contraction; otherwise item lt is tile lt
+  j.u0 = 0;
+  if constexpr (SPLIT) {
+    int tile, chunk;
+    split_item(lt, stage_tiles<STAGE>(d), tile, chunk);
+    j.K /= stage_split<STAGE>(d);
+    j.u0 = chunk * (j.K / kBK);
+    lt = tile;
   }
   if (sym) {
     sym_tile(lt, P / kTile, j.ti, j.tj);
@@ -1291,6 +1321,28 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   }
 }
 
+// fp32 partial tiles of a K-split stage: item (chunk c, tile t) of a matrix
+// with `tiles` tiles owns 256 KiB at kpart + (c·tiles + t)·65536 floats, as
+// [wave][accumulator quad][lane] float4s, so a wave's store of one quad (and
+// the reduce's load of it) is 1 KiB of consecutive memory.
+__device__ __forceinline__ f32x4* partial_at(float* kpart, int tiles, int tile, int chunk, int wave) {
+  return (f32x4*)kpart + (((int64_t)chunk * tiles + tile) * (kGemmThreads / 64) + wave) * (kQuads * 64);
+}
+
+// Chunk partial of work item lt (the matrix's item index) of a split stage.
+template <int STAGE, class D>
+__device__ __forceinline__ void store_partial(const D& d, int lt, const f32x4 (&acc)[kMi][kNi], int wave) {
+  typedef __attribute__((address_space(1))) f32x4 glb_f32x4;
+  const int tiles = stage_tiles<STAGE>(d);
+  int tile, chunk;
+  split_item(lt, tiles, tile, chunk);
+  glb_f32x4* dst = (glb_f32x4*)partial_at(d.kpart, tiles, tile, chunk, wave) + lane_id();
+#pragma unroll
+  for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < kNi; ++ni) dst[(mi * kNi + ni) * 64] = acc[mi][ni];
+}
+
 // Persistent GEMM launch: one block per CU (grid = min(tiles, CUs)), each
 // taking tiles from the queues until they are empty. The next tile's first
 // copies are issued before the current tile's epilogue, so its pipeline
@@ -1299,7 +1351,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 // during the previous epilogue and writes slot slot^1, which the waves read
 // after the barrier that ends the following tile's K loop; a slot is
 // rewritten only after every wave has passed the barrier that follows its read.
-template <int STAGE, int PDT, int LAYOUT>
+template <int STAGE, int PDT, int LAYOUT, bool SPLIT = false>
 __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char lds_a0[kOpBytes];
   __shared__ __attribute__((aligned(1024))) char lds_a1[kOpBytes];
@@ -1335,7 +1387,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
   static_assert(!kXT || (LAYOUT & kTiledX), "X read transposed needs the panel layout");
   auto prefetch = [&](const TileJob& j) { gemm_prefetch<kXT>(make_engine<kXT>(j, wave), ring); };
   int m = find_matrix(prefix, args.n, t);
-  TileJob job = decode_tile<STAGE, LAYOUT>(descs[m], t - prefix[m], args);
+  TileJob job = decode_tile<STAGE, LAYOUT, SPLIT>(descs[m], t - prefix[m], args);
   prefetch(job);
   for (;;) {
     f32x4 acc[kMi][kNi];
@@ -1346,13 +1398,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     TileJob jn{};
     if (tn >= 0) {
       mn = find_matrix(prefix, args.n, tn);
-      jn = decode_tile<STAGE, LAYOUT>(descs[mn], tn - prefix[mn], args);
+      jn = decode_tile<STAGE, LAYOUT, SPLIT>(descs[mn], tn - prefix[mn], args);
       prefetch(jn);
     }
     const bool leader = wave == 0 && lane_id() == 0;
     int after = -1;
     if (leader && tn >= 0) after = grab_tile(args.queues, total, &s_home);
-    gemm_epilogue<STAGE, PDT, LAYOUT>(args, descs[m], job, acc, wave, lds_stage[wave]);
+    if constexpr (SPLIT)
+      store_partial<STAGE>(descs[m], t - prefix[m], acc, wave);
+    else
+      gemm_epilogue<STAGE, PDT, LAYOUT>(args, descs[m], job, acc, wave, lds_stage[wave]);
     if (leader) s_tile[slot ^ 1] = after;
     if (tn < 0) break;
     t = tn;
@@ -1360,6 +1415,55 @@ __global__ __launch_bounds__(kGemmThreads, 1) void pm_ns_gemm_kernel(GemmArgs ar
     job = jn;
     slot ^= 1;
   }
+}
+
+// The second launch of a K-split stage: one single-wave block per (split
+// tile, wave sub-tile) of the group (prefix: prefix sums of each matrix's
+// split tiles, 0 for an unsplit matrix), so a tile's eight 128 x 64 sub-tiles
+// reduce on eight CUs. Each wave adds its accumulators' chunk partials in
+// chunk order (((p0 + p1) + p2) + p3, in fp32) and runs the stage's epilogue
+// on the sums, exactly as wave w of the unsplit launch runs it on its
+// accumulators (an epilogue wave needs no other wave of its block).
+template <int STAGE, int PDT, int LAYOUT>
+__global__ __launch_bounds__(64) void pm_ns_reduce_kernel(GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) char lds_stage[kStageBytes];
+  typedef const __attribute__((address_space(4))) MatDesc* DescPtr;
+  typedef const __attribute__((address_space(4))) int32_t* PrefixPtr;
+  typedef const __attribute__((address_space(1))) f32x4 glb_f32x4;
+  const DescPtr descs = (DescPtr)args.descs;
+  const PrefixPtr prefix = (PrefixPtr)args.prefix;
+  const int t = blockIdx.x / (kGemmThreads / 64), wave = blockIdx.x % (kGemmThreads / 64);
+  const int m = find_matrix(prefix, args.n, t);
+  const int lane = lane_id();
+  const int tile = t - prefix[m];
+  const TileJob job = decode_tile<STAGE, LAYOUT>(descs[m], tile, args);  // chunk 0 of the tile
+  const int tiles = stage_tiles<STAGE>(descs[m]), split = stage_split<STAGE>(descs[m]);
+  float* const kpart = descs[m].kpart;
+  // chunk by chunk, each chunk's 32 quads loaded together (one memory
+  // latency a chunk), added in chunk order
+  f32x4 acc[kMi][kNi];
+  {
+    const glb_f32x4* p0 = (const glb_f32x4*)partial_at(kpart, tiles, tile, 0, wave) + lane;
+#pragma unroll
+    for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < kNi; ++ni) acc[mi][ni] = p0[(mi * kNi + ni) * 64];
+  }
+#pragma unroll
+  for (int c = 1; c < kMaxKSplit; ++c) {
+    if (c >= split) break;
+    const glb_f32x4* pc = (const glb_f32x4*)partial_at(kpart, tiles, tile, c, wave) + lane;
+    f32x4 v[kMi][kNi];
+#pragma unroll
+    for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < kNi; ++ni) v[mi][ni] = pc[(mi * kNi + ni) * 64];
+#pragma unroll
+    for (int mi = 0; mi < kMi; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < kNi; ++ni) acc[mi][ni] += v[mi][ni];
+  }
+  gemm_epilogue<STAGE, PDT, LAYOUT>(args, descs[m], job, acc, wave, lds_stage);
 }
 
 // ============================================================ gram-form Q init

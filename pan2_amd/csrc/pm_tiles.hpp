@@ -92,6 +92,38 @@ PM_HD void sym_tile(int lt, int nt, int& ti, int& tj) {
   }
 }
 
+// K-split of one matrix's tiles in one stage: the number of chunks each tile's
+// K loop (kt units of 64) is cut into, the chunks' fp32 partial tiles then
+// summed in chunk order by a reduce launch. A function of the matrix's padded
+// shape and the stage only (tiles, kt), so a matrix steps to the same bits in
+// any group. A matrix splits only when its own tiles leave most of the chip
+// idle: tiles x chunks stays within one wave of 256 CUs, each chunk keeps at
+// least 16 units (a multiple of 4, the K loop's step; measured on a lone
+// 1024 x 4096, chunks of 4 or 8 units cost as much in partial traffic and the
+// reduce launch as they saved), at most 4 chunks, and never below Mp = 512, so
+// a small matrix and its 256-padded copy on the engine keep the same
+// arithmetic.
+constexpr int kMaxKSplit = 4;
+constexpr int kSplitMinMp = 512;
+constexpr int kSplitItems = 256;
+constexpr int kSplitMinUnits = 16;
+
+PM_HD int k_split(int mp, int tiles, int kt) {
+  if (mp < kSplitMinMp || tiles <= 0 || kt % 4) return 1;
+  int s = 1;
+  while (2 * s <= kMaxKSplit && (kt / 4) % (2 * s) == 0 && kt / (2 * s) >= kSplitMinUnits &&
+         tiles * 2 * s <= kSplitItems)
+    s *= 2;
+  return s;
+}
+
+// Work item lt of a matrix whose tiles are split into s chunks: chunk-major,
+// so the items an XCD runs together share their chunk's K range.
+PM_HD void split_item(int lt, int tiles, int& tile, int& chunk) {
+  chunk = lt / tiles;
+  tile = lt - chunk * tiles;
+}
+
 // Element offset of (r, c) in a workspace matrix with ld columns.
 // Row-major: r·ld + c. Panel layout (tiled): the matrix is cut into panels of
 // 256 rows (the GEMM tile) and each panel into units of 64 columns; unit

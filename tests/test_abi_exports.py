@@ -253,17 +253,38 @@ def ws_bytes(lib, ms, limit=0):
     return lib.pm_workspace_bytes(arr(*ms), len(ms), ctypes.byref(hp))
 
 
+def k_split_partial_bytes(mp, np_):
+    """fp32 partial tiles a matrix's K-split stages need: the largest stage's
+    tiles x chunks x 256 KiB (the rule of pan2_amd/csrc/pm_tiles.hpp::k_split,
+    whose invariants tests/native/tile_order_check.cpp checks)."""
+    def k_split(tiles, kt):
+        if mp < 512 or kt % 4:
+            return 1
+        s = 1
+        while 2 * s <= 4 and (kt // 4) % (2 * s) == 0 and kt // (2 * s) >= 16 and tiles * 2 * s <= 256:
+            s *= 2
+        return s
+    nt = mp // 256
+    sym, full = nt * (nt + 1) // 2, nt * (np_ // 256)
+    stages = [(sym, k_split(sym, np_ // 64)), (sym, k_split(sym, mp // 64)), (full, k_split(full, mp // 64))]
+    return max([t * s * 256 * 256 * 4 for t, s in stages if s > 1] or [0])
+
+
 def test_workspace_sizing(lib):
     one = ws_bytes(lib, [mat(1024, 4096)])
     assert one > 0 and one % 256 == 0
     assert ws_bytes(lib, [mat(4096, 1024)]) == one, "a tall matrix is planned as its transpose"
-    # bf16 X x2 (ping-pong; no transposed copy) + A + B dominate: 2*M*N*2 + 2*M*M*2 bytes
+    # bf16 X x2 (ping-pong; no transposed copy) + A + B + the K-split partials
+    # (1024 x 4096 splits its gram: 10 tiles x 4 chunks x 256 KiB) dominate
     M, N = 1024, 4096
-    assert 2 * M * N * 2 + 2 * M * M * 2 <= one <= 2 * M * N * 2 + 2 * M * M * 2 + (1 << 20)
+    kp = k_split_partial_bytes(M, N)
+    assert kp == 10 * 4 * 256 * 1024
+    assert k_split_partial_bytes(4096, 5120) == 0 and k_split_partial_bytes(256, 4096) == 0
+    assert 2 * M * N * 2 + 2 * M * M * 2 + kp <= one <= 2 * M * N * 2 + 2 * M * M * 2 + kp + (1 << 20)
     # padding to 256: 300x700 is planned as 512x768
     assert ws_bytes(lib, [mat(300, 700)]) == ws_bytes(lib, [mat(512, 768)])
     three = ws_bytes(lib, [mat(1024, 4096)] * 3)
-    table1 = one - (2 * M * N * 2 + 2 * M * M * 2 + ((M // 64) * (N // 64) * 4 + 255) // 256 * 256 + 256)
+    table1 = one - (2 * M * N * 2 + 2 * M * M * 2 + ((M // 64) * (N // 64) * 4 + 255) // 256 * 256 + 256 + kp)
     assert table1 > 0
     assert three > 3 * (one - table1)
     # a cap below the total keeps room for the largest matrix only (groups run in turn)

@@ -40,9 +40,28 @@ def gemm_kernels(asm):
     for m in re.finditer(r"^(_ZN2pm17pm_ns_gemm_kernel\w+):.*$", asm, flags=re.M):
         body = asm[m.end():]
         kernels[m.group(1)] = body[:body.index("s_endpgm")].split("\n")
-    # panel layout: GRAM, POLY, UPDATE, FINAL x {f32, bf16}; row-major: GRAM, POLY (pm_gram, pm_gemm_symmetric)
-    assert len(kernels) == 7, sorted(kernels)
+    # panel layout: GRAM, POLY, UPDATE, FINAL x {f32, bf16}, each also as its
+    # K-split instantiation (chunk partials instead of the epilogue); row-major:
+    # GRAM, POLY (pm_gram, pm_gemm_symmetric)
+    assert len(kernels) == 12, sorted(kernels)
+    assert sum(1 for k in kernels if k.endswith("ELb1EEEvNS_8GemmArgsE")) == 5, sorted(kernels)
     return kernels
+
+
+@pytest.fixture(scope="module")
+def reduce_kernels(asm):
+    kernels = {}
+    for m in re.finditer(r"^(_ZN2pm19pm_ns_reduce_kernel\w+):.*$", asm, flags=re.M):
+        body = asm[m.end():]
+        kernels[m.group(1)] = body[:body.index("s_endpgm")].split("\n")
+    assert len(kernels) == 5, sorted(kernels)  # GRAM, POLY, UPDATE, FINAL x {f32, bf16}
+    return kernels
+
+
+def test_reduce_kernels_have_no_scratch(reduce_kernels):
+    for name, lines in reduce_kernels.items():
+        n = sum(1 for ln in lines if "scratch_" in ln)
+        assert n == 0, f"{name}: {n} scratch instructions"
 
 
 def _regs(tok):
