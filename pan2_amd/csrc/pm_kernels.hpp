@@ -941,7 +941,7 @@ __device__ __forceinline__ int xcc_id() {
 //          products of pan/optim/patch_muon.py:320-331
 //   UPDATE X' = s·(a·X + S[sl] X)  (torch.addmm(X, B, X, beta=a), :66; a = 0 is
 //                                   the gram form's X <- Q X, :316), written
-//                                   as X' and X'ᵀ
+//                                   as X' (X is read transposed from LDS)
 //   FINAL  O = bf16(s·(a·X + S[sl] X)) then p <- p·(1-lr·wd) - lr·adj·O
 //          (pan/optim/muon_triton.py:130-131), or O stored (MODE_NS)
 // GRAM and SYMM are symmetric: only upper-triangle tiles are computed and

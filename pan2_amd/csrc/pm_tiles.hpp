@@ -49,8 +49,8 @@ PM_HD void full_tile(int lt, int np, int nq, int& ti, int& tj) {
 // The same np x nq grid walked column group by column group: kGroupCols
 // columns at a time, and within a column group kGroupRows rows at a time
 // (each such block column by column), so the kXcds blocks that run at once go
-// down the rows of the same columns. For C = S·X, whose right operand (Xᵀ
-// panels, one per tile column) is the large one, the XCDs then read the same
+// down the rows of the same columns. For C = S·X, whose right operand (X's
+// 256-column blocks, one per tile column) is the large one, the XCDs then read the same
 // few column panels at the same time and the memory-side cache serves the
 // repeats: each panel comes from HBM about once instead of once per row group.
 constexpr int kGroupCols = 8;
