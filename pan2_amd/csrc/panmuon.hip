@@ -382,8 +382,6 @@ struct Launcher {
     a.queues = queues + kXcds * launch++;
     return PM_OK;
   }
-  // The GEMM launch of one stage over the group's work items, then, when some
-  // matrix splits this stage, the reduce launch over its split tiles.
   // The launches of one stage: the GEMM over unsplit matrices' tiles; then,
   // when some matrix splits this stage, the GEMM over their chunk items
   // (fp32 partials) and the reduce over their tiles. The stage's FLOPs go
