@@ -7,7 +7,6 @@ or fails to load, every entry point raises.
 from __future__ import annotations
 
 import ctypes
-import operator
 import os
 import threading
 
@@ -484,7 +483,7 @@ def _device_scalar(t, what: str, dev):
     return t.data_ptr()
 
 
-# numpy twin of PmAdamTensor, filled list by list
+# numpy twin of PmAdamTensor (the array _pm_host.fill_adam writes)
 _PM_ADAM_NP = np.dtype({
     "names": [f for f, _ in PmAdamTensor._fields_],
     "formats": ["u8", "u8", "u8", "u8", "u8", "u8", "i8", "i4", "i4", "i4", "i4"],
@@ -495,6 +494,24 @@ _PM_ADAM_NP = np.dtype({
 
 ADAM_DTYPES = {torch.float32: PM_DTYPE_F32, torch.bfloat16: PM_DTYPE_BF16, torch.float16: PM_DTYPE_F16}
 
+_host = None
+
+
+def host_ext():
+    """The _pm_host extension (pan2_amd/csrc/pm_host.cpp, built beside libpanmuon
+    by pan2_amd.build): fills pm_adam_tensor arrays from torch's tensor lists."""
+    global _host
+    if _host is None:
+        try:
+            from . import _pm_host
+        except ImportError as e:
+            raise RuntimeError("pan2_amd._pm_host is not built; run `python -m pan2_amd.build`") from e
+        if _pm_host.DESC_BYTES != ctypes.sizeof(PmAdamTensor):
+            raise RuntimeError(f"_pm_host's pm_adam_tensor is {_pm_host.DESC_BYTES} bytes, "
+                               f"ctypes' {ctypes.sizeof(PmAdamTensor)}: rebuild")
+        _host = _pm_host
+    return _host
+
 
 def adam_dtype_code(t: torch.Tensor) -> int:
     """pm_adam_step's dtype code of a tensor: float32, bfloat16 or float16."""
@@ -504,18 +521,18 @@ def adam_dtype_code(t: torch.Tensor) -> int:
     return code
 
 
-_dtype_of = operator.attrgetter("dtype")
-_data_ptr = torch.Tensor.data_ptr
-_numel = torch.Tensor.numel
-
-
-def _dtype_codes(ts, kinds=None) -> int | list[int]:
-    """One code for a list of one dtype, else one code per tensor. kinds: the
-    list's set of dtypes, when the caller has taken it already."""
-    kinds = set(map(_dtype_of, ts)) if kinds is None else kinds
-    if len(kinds) == 1:
-        return adam_dtype_code(ts[0])
-    return [adam_dtype_code(t) for t in ts]
+def adam_descs(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps):
+    """The pm_adam_tensor array of one call, filled in one C++ pass, or None
+    when some tensor is off params[0]'s HIP device or of a dtype pm_adam_step
+    does not take (float32 / bfloat16 / float16; max_exp_avg_sq of
+    exp_avg_sq's dtype; float32 steps). max_exp_avg_sqs: [] without amsgrad.
+    Raises ValueError for a grad that is not contiguous."""
+    h = host_ext()
+    arr = np.empty(len(params), dtype=_PM_ADAM_NP)
+    rc = h.fill_adam(arr.ctypes.data, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps)
+    if rc == h.GRAD_NOT_CONTIGUOUS:
+        raise ValueError("grads must be contiguous")
+    return arr if rc == h.FILLED else None
 
 
 def _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev):
@@ -529,6 +546,7 @@ def _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, sta
                 raise ValueError(f"{what} must be contiguous")
             if t.shape != p.shape:
                 raise ValueError(f"{what} shape {tuple(t.shape)} differs from the param's {tuple(p.shape)}")
+            adam_dtype_code(t)
         st = state_steps[i]
         if st.device != dev or st.dtype != torch.float32 or st.numel() != 1:
             raise ValueError("state steps must be 1-element float32 tensors on the params' device")
@@ -538,15 +556,14 @@ def _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, sta
 
 def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, *, lr, beta1: float,
               beta2: float, eps: float, weight_decay: float, amsgrad: bool, maximize: bool, decoupled: bool,
-              grad_scale=None, found_inf=None, trusted: bool = False, dtype_sets=None) -> None:
+              grad_scale=None, found_inf=None, trusted: bool = False) -> None:
     """pm_adam_step over matching lists of contiguous device tensors (updated
     in place, steps included). lr: float, or a 1-element tensor (read on the
-    device when it lives there). trusted: the lists come from torch's Adam,
-    whose _init_group already guarantees one device, matching shapes,
-    contiguous state and float32 device steps; only the per-call checks run.
-    dtype_sets: the set of dtypes of params, grads, exp_avgs and exp_avg_sqs,
-    when the caller has taken them already (the descriptors need them)."""
-    lib = load()
+    device when it lives there). max_exp_avg_sqs: read with amsgrad only.
+    trusted: the lists come from torch's Adam, whose _init_group already
+    guarantees one device, matching shapes, contiguous state and float32
+    device steps; the descriptor pass still checks devices, dtypes and the
+    grads' contiguity."""
     n = len(params)
     if n == 0:
         return
@@ -555,24 +572,20 @@ def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps
         raise RuntimeError("pan2_amd Adam runs on HIP device tensors only; got a CPU parameter")
     if not trusted:
         _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev)
-    elif not all(map(torch.Tensor.is_contiguous, grads)):
-        raise ValueError("grads must be contiguous")
-    kinds = dtype_sets if dtype_sets is not None else (None,) * 4
-    # map() over the unbound methods keeps the per-tensor loop in C: this
-    # list building is most of the host time of a step over a few hundred tensors
-    arr = np.zeros(n, dtype=_PM_ADAM_NP)
-    arr["param"] = list(map(_data_ptr, params))
-    arr["grad"] = list(map(_data_ptr, grads))
-    arr["exp_avg"] = list(map(_data_ptr, exp_avgs))
-    arr["exp_avg_sq"] = list(map(_data_ptr, exp_avg_sqs))
-    if amsgrad:
-        arr["max_exp_avg_sq"] = list(map(_data_ptr, max_exp_avg_sqs))
-    arr["step"] = list(map(_data_ptr, state_steps))
-    arr["numel"] = list(map(_numel, params))
-    arr["param_dtype"] = _dtype_codes(params, kinds[0])
-    arr["grad_dtype"] = _dtype_codes(grads, kinds[1])
-    arr["exp_avg_dtype"] = _dtype_codes(exp_avgs, kinds[2])
-    arr["exp_avg_sq_dtype"] = _dtype_codes(exp_avg_sqs, kinds[3])
+    arr = adam_descs(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs if amsgrad else [], state_steps)
+    if arr is None:
+        raise ValueError("pm_adam_step takes float32 / bfloat16 / float16 tensors on one HIP device, "
+                         "max_exp_avg_sq of exp_avg_sq's dtype and float32 steps")
+    adam_launch(arr, dev, lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+                maximize=maximize, decoupled=decoupled, grad_scale=grad_scale, found_inf=found_inf)
+
+
+def adam_launch(arr, dev, *, lr, beta1: float, beta2: float, eps: float, weight_decay: float, amsgrad: bool,
+                maximize: bool, decoupled: bool, grad_scale=None, found_inf=None) -> None:
+    """pm_adam_step over a filled pm_adam_tensor array (adam_descs) of tensors
+    on device dev, on its current stream."""
+    lib = load()
+    n = len(arr)
     keep = [arr]
     hp = PmAdamHparams(beta1=float(beta1), beta2=float(beta2), eps=float(eps), weight_decay=float(weight_decay),
                        amsgrad=int(bool(amsgrad)), maximize=int(bool(maximize)),

@@ -20,7 +20,6 @@ unpatched process would run them; fp32, bf16 and fp16 device tensors go to
 from __future__ import annotations
 
 import importlib
-import operator
 
 import torch
 from torch import Tensor
@@ -31,9 +30,6 @@ from .. import _lib
 _adam_module = importlib.import_module("torch.optim.adam")
 # torch's own fused Adam, for the tensors pm_adam_step does not take
 _torch_fused_adam = _adam_module._fused_adam
-
-_get_device = Tensor.get_device
-_dtype_of = operator.attrgetter("dtype")
 
 
 def _scalar(x):
@@ -76,24 +72,22 @@ def _fused_adam(
     if differentiable:
         raise RuntimeError("Adam with fused=True does not support differentiable=True")
     beta1, beta2 = _scalar(beta1), _scalar(beta2)
-    # The common case, scanned list by list: every tensor on one HIP device
-    # (get_device is -1 on the CPU) with a dtype pm_adam_step takes.
-    lists = (params, grads, exp_avgs, exp_avg_sqs) + ((max_exp_avg_sqs,) if amsgrad else ())
-    devs = [set(map(_get_device, xs)) for xs in lists]
-    kinds = [set(map(_dtype_of, xs)) for xs in lists]
-    if (params[0].is_cuda and len(devs[0]) == 1 and all(d == devs[0] for d in devs)
-            and all(k <= _lib.ADAM_DTYPES.keys() for k in kinds)):
+    # The common case, checked and turned into descriptors in one C++ pass:
+    # every tensor on params[0]'s HIP device with a dtype pm_adam_step takes.
+    arr = None
+    if params[0].is_cuda:
+        arr = _lib.adam_descs(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs if amsgrad else [],
+                              state_steps)
+    if arr is not None:
         dev = params[0].device
         dev_lr = lr
         if isinstance(lr, Tensor) and lr.device.type != "cpu" and lr.device != dev:
             dev_lr = lr.to(device=dev, non_blocking=True)
-        _lib.adam_step(
-            params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs if amsgrad else [None] * len(params), state_steps,
-            lr=dev_lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+        _lib.adam_launch(
+            arr, dev, lr=dev_lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
             maximize=maximize, decoupled=decoupled_weight_decay,
             grad_scale=None if grad_scale is None else grad_scale.to(dev, non_blocking=True),
             found_inf=None if found_inf is None else found_inf.to(dev, non_blocking=True),
-            trusted=True, dtype_sets=kinds[:4],
         )
         return
     mine = [_native(i, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, amsgrad) for i in range(len(params))]
@@ -121,7 +115,7 @@ def _fused_adam(
             dev_lr = lr.to(device=dev, non_blocking=True)
         _lib.adam_step(
             pick(params), pick(grads), pick(exp_avgs), pick(exp_avg_sqs),
-            pick(max_exp_avg_sqs) if amsgrad else [None] * len(idx), pick(state_steps),
+            pick(max_exp_avg_sqs) if amsgrad else [], pick(state_steps),
             lr=dev_lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
             maximize=maximize, decoupled=decoupled_weight_decay,
             grad_scale=None if grad_scale is None else grad_scale.to(dev, non_blocking=True),
@@ -133,7 +127,9 @@ def _fused_adam(
 def patch_adamw() -> None:
     """Install the HIP path behind every ``fused=True`` Adam / AdamW step.
 
-    Loads libpanmuon first, so a missing or broken build fails here, loudly.
+    Loads libpanmuon and the _pm_host extension first, so a missing or broken
+    build fails here, loudly.
     """
     _lib.load()
+    _lib.host_ext()
     _adam_module._fused_adam = _fused_adam

@@ -217,3 +217,51 @@ def test_lr_scheduler_base_lrs_assignment_recaptured(restore_torch_muon):
     sched.step()
     assert sched.get_last_lr() == [pytest.approx(0.8 * 0.5)]
     assert reads == [1]
+
+
+def test_adam_descriptor_pass_layout_and_statuses():
+    """_pm_host.fill_adam (pan2_amd/csrc/pm_host.cpp) on CPU tensors (hip_only
+    off): every field of the pm_adam_tensor array _lib hands to pm_adam_step,
+    read back through the ctypes layout; and the statuses the AdamW path
+    branches on."""
+    import ctypes
+
+    import numpy as np
+
+    from pan2_amd import _lib
+
+    h = _lib.host_ext()
+    assert h.DESC_BYTES == ctypes.sizeof(_lib.PmAdamTensor) == 72
+    dts = [torch.float32, torch.bfloat16, torch.float16]
+    ps = [torch.zeros(5 + 3 * i, dtype=dts[i % 3]) for i in range(7)]
+    gs = [torch.zeros(p.shape, dtype=dts[(i + 1) % 3]) for i, p in enumerate(ps)]
+    ms = [torch.zeros(p.shape, dtype=dts[(i + 2) % 3]) for i, p in enumerate(ps)]
+    vs = [torch.zeros(p.shape, dtype=dts[i % 3]) for i, p in enumerate(ps)]
+    xs = [torch.zeros_like(v) for v in vs]
+    st = [torch.zeros((), dtype=torch.float32) for _ in ps]
+    for ams in (False, True):
+        arr = np.zeros(len(ps), dtype=_lib._PM_ADAM_NP)
+        assert h.fill_adam(arr.ctypes.data, ps, gs, ms, vs, xs if ams else [], st, hip_only=False) == h.FILLED
+        c = (_lib.PmAdamTensor * len(ps)).from_address(arr.ctypes.data)
+        for i in range(len(ps)):
+            assert (c[i].param, c[i].grad, c[i].exp_avg, c[i].exp_avg_sq, c[i].step) == (
+                ps[i].data_ptr(), gs[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(), st[i].data_ptr())
+            assert (c[i].max_exp_avg_sq or 0) == (xs[i].data_ptr() if ams else 0)
+            assert c[i].numel == ps[i].numel()
+            assert [c[i].param_dtype, c[i].grad_dtype, c[i].exp_avg_dtype, c[i].exp_avg_sq_dtype] == [
+                _lib.adam_dtype_code(t) for t in (ps[i], gs[i], ms[i], vs[i])]
+    arr = np.zeros(len(ps), dtype=_lib._PM_ADAM_NP)
+    # the product path takes HIP tensors only: CPU lists are the general path's
+    assert h.fill_adam(arr.ctypes.data, ps, gs, ms, vs, [], st) == h.GENERAL
+    assert _lib.adam_descs(ps, gs, ms, vs, [], st) is None
+    # a dtype pm_adam_step does not take, float64 steps, a max_exp_avg_sq of another dtype
+    for bad in ({"p": torch.zeros(4, dtype=torch.float64)}, {"s": torch.zeros((), dtype=torch.float64)},
+                {"x": torch.zeros(ps[0].shape, dtype=torch.float64)}):
+        p2, s2, x2 = [bad.get("p", ps[0])] + ps[1:], [bad.get("s", st[0])] + st[1:], [bad.get("x", xs[0])] + xs[1:]
+        assert h.fill_adam(arr.ctypes.data, p2, gs, ms, vs, x2 if "x" in bad else [], s2, hip_only=False) == h.GENERAL
+    nc = [torch.zeros(4, 6)[:, ::2]] + gs[1:]
+    assert h.fill_adam(arr.ctypes.data, [torch.zeros(4, 3)] + ps[1:], nc, ms, vs, [], st,
+                       hip_only=False) == h.GRAD_NOT_CONTIGUOUS
+    with pytest.raises(RuntimeError, match="differ in length"):
+        h.fill_adam(arr.ctypes.data, ps, gs[:-1], ms, vs, [], st, hip_only=False)
+    assert h.fill_adam(0, [], [], [], [], [], []) == h.FILLED
