@@ -736,7 +736,6 @@ __device__ __forceinline__ void sm_pro_tiles(const ProArgs& args, const ProMat& 
     else
       sm_pro_fetch(pm, args.mode == MODE_STEP, tj, h, half, wq, gvec, mvec, raw);
   };
-  const bool step = args.mode == MODE_STEP;
   const int wave = 4 * half + wq, lane = lane_id();
   const int r0 = half * 64, c0 = wq * 32;
   const int ntiles = nrun * kProRun;
@@ -806,7 +805,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void pm_small_prologue_kernel(ProA
   const int wave = wave_id(), lane = lane_id();
   const int half = wave >> 2, wq = wave & 3;
   const int r0 = (wave >> 2) * 64, c0 = (wave & 3) * 32;
-  const int nrun = uni32(d.Np) / (kProTile * kProRun), ntiles = nrun * kProRun;
+  const int nrun = uni32(d.Np) / (kProTile * kProRun);
   float* const partials = (float*)uni64((int64_t)d.partials);
   const bool step = args.mode == MODE_STEP;
   const bool mvec_any = step && vec_ok(pm.mom, pm.m_dt, pm.m_ld);

@@ -13,7 +13,6 @@ show that each check can fail.
 """
 from __future__ import annotations
 
-import math
 
 import numpy as np
 import torch

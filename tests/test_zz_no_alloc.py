@@ -4,7 +4,6 @@ descriptor tables as kernel arguments) gives bit-identical params and momentum
 buffers to pm_muon_step on the same inputs. Two calls in a row, the second
 with a smaller input that runs in the scratch the first call left behind.
 """
-import ctypes
 
 import pytest
 import torch
