@@ -82,3 +82,27 @@ def test_nonfinite_matrix_in_a_fused_small_group(form):
             assert torch.isnan(got[i].float()).all(), i
         else:
             assert torch.equal(got[i], clean[i]), i
+
+
+@pytest.mark.parametrize("form", ["standard", "gram"])
+def test_nonfinite_through_k_split_stages(form):
+    """Matrices whose stages run K-split (fp32 chunk partials, then the
+    reduce launch; 2048 x 2048 splits every stage, 1024 x 4096 its grams), one
+    holding a NaN and one an Inf, beside finite split and unsplit matrices:
+    the two come out all NaN (the same products spread it as in the shapes
+    above, where torch's NS is checked), the rest bit-identical to the
+    all-finite call."""
+    shapes = [(2048, 2048), (1024, 4096), (4096, 1024), (2048, 2048), (512, 768)]
+    xs = [seeded(s, 40 + i).to(DEV) for i, s in enumerate(shapes)]
+    clean = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shapes]
+    _lib.newton_schulz_into(list(zip(xs, clean)), ns_form=form)
+    bad = {0: float("nan"), 2: float("inf")}
+    for i, v in bad.items():
+        xs[i][700, 300] = v
+    got = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shapes]
+    _lib.newton_schulz_into(list(zip(xs, got)), ns_form=form)
+    for i in range(len(shapes)):
+        if i in bad:
+            assert torch.isnan(got[i].float()).all(), i
+        else:
+            assert torch.equal(got[i], clean[i]), i
