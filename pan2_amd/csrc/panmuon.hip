@@ -64,9 +64,9 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 struct Plan {
   int32_t rows, cols, trans, M, N, Mp, Np;
   bool small;
-  int32_t ks_gram, ks_symm, ks_full;  // K-split chunks per tile (k_split), 1: unsplit
+  int32_t ks_gram, ks_symm, ks_full;  // K-split chunks per tile (split_call), 1: unsplit
   size_t kpart;                       // bytes of fp32 partial tiles (the largest split stage's)
-  size_t ws;  // workspace bytes of this matrix
+  size_t ws;  // workspace bytes of this matrix (with kpart once split_call has run)
   double flops;
 };
 
@@ -88,20 +88,11 @@ Plan make_plan(int64_t rows, int64_t cols, int form) {
   const size_t x = align_up((size_t)p.Mp * p.Np * 2);
   const size_t a = align_up((size_t)p.Mp * p.Mp * 2);
   const size_t part = align_up((size_t)(p.Mp / kProTile) * (p.Np / kProTile) * 4);  // (covers every run count)
-  // K-split of each GEMM stage (engine matrices only): GRAM contracts over Np,
-  // the symmetric products and UPDATE / FINAL over Mp
-  const int32_t nt = p.Mp / kTile, sym = nt * (nt + 1) / 2, full = nt * (p.Np / kTile);
-  p.ks_gram = p.small ? 1 : k_split(p.Mp, sym, p.Np / 64);
-  p.ks_symm = p.small ? 1 : k_split(p.Mp, sym, p.Mp / 64);
-  p.ks_full = p.small ? 1 : k_split(p.Mp, full, p.Mp / 64);
-  size_t kp = 0;
-  const size_t tile_bytes = (size_t)kTile * kTile * 4;
-  if (p.ks_gram > 1) kp = std::max(kp, (size_t)sym * p.ks_gram * tile_bytes);
-  if (p.ks_symm > 1) kp = std::max(kp, (size_t)sym * p.ks_symm * tile_bytes);
-  if (p.ks_full > 1) kp = std::max(kp, (size_t)full * p.ks_full * tile_bytes);
-  p.kpart = kp;
-  // X ping-pong, the square work matrices, the prologue partials, the K-split partials
-  p.ws = 2 * x + (size_t)square_bufs(form, p.small) * a + part + kAlign + kp;
+  // X ping-pong, the square work matrices, the prologue partials; split_call
+  // adds the K-split partials
+  p.ks_gram = p.ks_symm = p.ks_full = 1;
+  p.kpart = 0;
+  p.ws = 2 * x + (size_t)square_bufs(form, p.small) * a + part + kAlign;
   const double M = p.M, N = p.N;
   p.flops = M * (M + 1) * N + M * M * (M + 1) + 2 * M * M * N;
   return p;
@@ -188,6 +179,41 @@ struct Item {
   Plan plan;
   MatDesc desc;
 };
+
+// K-split of a call's engine matrices (k_split in pm_tiles.hpp). A stage
+// splits only when all of the call's engine matrices together hold so few of
+// its tiles that most of the chip would sit idle; each matrix then cuts its
+// tiles into as many chunks as its shape allows within that budget. On a call
+// whose tiles fill the chip, the chunks' fp32 partials would cost more than
+// the idle CUs they fill (measured: 48 x 2048² runs 8.0 ms unsplit, 15.7 ms
+// split). The choice depends on the call only, so a call gives the same bits
+// in any workspace grouping and through either step entry point. GRAM
+// contracts over Np, the symmetric products and UPDATE / FINAL over Mp.
+void split_call(std::vector<Item>& items) {
+  int64_t tiles[3] = {0, 0, 0};
+  for (const Item& it : items)
+    if (!it.plan.small) {
+      tiles[0] += sym_tiles(it.plan);
+      tiles[1] += sym_tiles(it.plan);
+      tiles[2] += full_tiles(it.plan);
+    }
+  int call[3];
+  for (int st = 0; st < 3; ++st) call[st] = (int)std::min<int64_t>(tiles[st], kSplitItems + 1);
+  const size_t tile_bytes = (size_t)kTile * kTile * 4;
+  for (Item& it : items) {
+    Plan& p = it.plan;
+    if (p.small) continue;
+    p.ks_gram = k_split(p.Mp, call[0], p.Np / 64);
+    p.ks_symm = k_split(p.Mp, call[1], p.Mp / 64);
+    p.ks_full = k_split(p.Mp, call[2], p.Mp / 64);
+    size_t kp = 0;
+    if (p.ks_gram > 1) kp = std::max(kp, (size_t)sym_tiles(p) * p.ks_gram * tile_bytes);
+    if (p.ks_symm > 1) kp = std::max(kp, (size_t)sym_tiles(p) * p.ks_symm * tile_bytes);
+    if (p.ks_full > 1) kp = std::max(kp, (size_t)full_tiles(p) * p.ks_full * tile_bytes);
+    p.kpart = kp;
+    p.ws += kp;
+  }
+}
 
 // Descriptor uploads go through pinned staging buffers: the host table is
 // copied into one, and an asynchronous copy on the caller's stream moves it
@@ -832,6 +858,7 @@ int collect_step(const pm_matrix* mats, int n, int form, std::vector<Item>& item
     d.adj_ratio = (float)m.adj_ratio;
     items.push_back(it);
   }
+  split_call(items);
   return PM_OK;
 }
 
@@ -854,6 +881,7 @@ int collect_ns(const pm_ns_matrix* mats, int n, int form, std::vector<Item>& ite
     d.p_dt = PM_DTYPE_BF16; d.g_dt = m.in_dtype; d.m_dt = PM_DTYPE_F32;
     items.push_back(it);
   }
+  split_call(items);
   return PM_OK;
 }
 

@@ -94,15 +94,14 @@ PM_HD void sym_tile(int lt, int nt, int& ti, int& tj) {
 
 // K-split of one matrix's tiles in one stage: the number of chunks each tile's
 // K loop (kt units of 64) is cut into, the chunks' fp32 partial tiles then
-// summed in chunk order by a reduce launch. A function of the matrix's padded
-// shape and the stage only (tiles, kt), so a matrix steps to the same bits in
-// any group. A matrix splits only when its own tiles leave most of the chip
-// idle: tiles x chunks stays within one wave of 256 CUs, each chunk keeps at
-// least 16 units (a multiple of 4, the K loop's step; measured on a lone
-// 1024 x 4096, chunks of 4 or 8 units cost as much in partial traffic and the
-// reduce launch as they saved), at most 4 chunks, and never below Mp = 512, so
-// a small matrix and its 256-padded copy on the engine keep the same
-// arithmetic.
+// summed in chunk order by a reduce launch. `tiles` is the stage's tile count
+// over every engine matrix of the call (the launcher's split_call), so only a
+// call that would leave most of the chip idle splits: tiles x chunks stays
+// within one wave of 256 CUs. Each chunk keeps at least 16 units (a multiple
+// of 4, the K loop's step; measured on a lone 1024 x 4096, chunks of 4 or 8
+// units cost as much in partial traffic and the reduce launch as they saved),
+// at most 4 chunks, and never below Mp = 512, so a small matrix and its
+// 256-padded copy on the engine keep the same arithmetic.
 constexpr int kMaxKSplit = 4;
 constexpr int kSplitMinMp = 512;
 constexpr int kSplitItems = 256;

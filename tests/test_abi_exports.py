@@ -293,6 +293,22 @@ def test_workspace_sizing(lib):
     assert ws_bytes(lib, [mat(pdt=5)]) == 0 and "dtype" in _lib.last_error()
 
 
+def test_k_split_is_decided_per_call(lib):
+    """The K-split depends on the call (pan2_amd/csrc/panmuon.hip::split_call):
+    a lone 2048 x 2048 splits every stage and holds the largest stage's partials
+    (64 UPDATE tiles x 2 chunks x 256 KiB); 48 of them in one call fill the chip,
+    none splits and none holds partials; a workspace cap that groups the call
+    does not change that."""
+    kp = 64 * 2 * 256 * 1024
+    one = ws_bytes(lib, [mat(2048, 2048)])
+    many = ws_bytes(lib, [mat(2048, 2048)] * 48)
+    assert 48 * (one - kp) - 48 * (1 << 20) <= many <= 48 * (one - kp) + (1 << 20)
+    two = ws_bytes(lib, [mat(2048, 2048)] * 2)  # 72 gram tiles: still split 2 ways
+    assert 2 * one - (1 << 20) <= two <= 2 * one + (1 << 20)
+    capped = ws_bytes(lib, [mat(2048, 2048)] * 48, limit=1)  # groups of one matrix: still unsplit
+    assert capped < one - kp + (1 << 20)
+
+
 def test_gram_form_workspace_sizing(lib):
     M, N = 1024, 4096
     std = ws_bytes(lib, [mat(M, N)])

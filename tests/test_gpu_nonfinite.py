@@ -87,8 +87,9 @@ def test_nonfinite_matrix_in_a_fused_small_group(form):
 @pytest.mark.parametrize("form", ["standard", "gram"])
 def test_nonfinite_through_k_split_stages(form):
     """Matrices whose stages run K-split (fp32 chunk partials, then the
-    reduce launch; 2048 x 2048 splits every stage, 1024 x 4096 its grams), one
-    holding a NaN and one an Inf, beside finite split and unsplit matrices:
+    reduce launch; in this call the grams of the 2048 x 2048 and 1024 x 4096
+    matrices and the 2048 x 2048 symmetric products split), one holding a NaN and one an Inf, beside finite split and
+    unsplit matrices:
     the two come out all NaN (the same products spread it as in the shapes
     above, where torch's NS is checked), the rest bit-identical to the
     all-finite call."""

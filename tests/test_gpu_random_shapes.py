@@ -7,8 +7,9 @@ padded panels run), long sides up to 3000, wide and tall, none a multiple of
 units are exercised). One pm_newton_schulz call takes all of them (mixed small
 and large groups, several workspace groups under a small cap); each output is
 checked against a float32 restatement of the standard quintic on the GPU
-(TORCH/optim/_muon.py:55-69), and a second call with every matrix on its own
-must give the same bits (grouping changes no arithmetic).
+(TORCH/optim/_muon.py:55-69). The same call in one workspace group must give
+the same bits (grouping changes no arithmetic), and so must each matrix on its
+own wherever its K-split, which depends on the call's size, is the call's.
 
 The gram form (PAN 2's production form) gets its own sweep of 20 smaller
 shapes, gated as in the gram-form tests: against the fp64 standard NS within
@@ -28,6 +29,7 @@ from torch.optim._muon import _zeropower_via_newtonschulz as torch_ns
 
 from oracle import muon_ref
 from pan2_amd import _lib
+from tests.ksplit_rule import call_splits
 
 pytestmark = pytest.mark.gpu
 
@@ -77,11 +79,20 @@ def test_random_ragged_shapes_one_call():
         ref_cpu = ref.cpu()
         err_torch = float((torch_ns(x.cpu(), COEFFS, 5, 1e-7).double() - ref_cpu).norm() / ref_cpu.norm())
         assert err <= max(2e-2, 1.25 * err_torch), (s, err, err_torch)
-    singles = [torch.empty_like(o) for o in outs]
-    for x, o in zip(xs, singles):
-        _lib.newton_schulz_into([(x, o)], ns_coefficients=COEFFS)
-    for s, o, o1 in zip(shp, outs, singles):
+    # the same call in one workspace group: the same bits
+    whole = [torch.empty_like(o) for o in outs]
+    _lib.newton_schulz_into(list(zip(xs, whole)), ns_coefficients=COEFFS)
+    for s, o, o1 in zip(shp, outs, whole):
         assert torch.equal(o, o1), s
+    # each matrix alone: the same bits wherever its K-split is the call's
+    call = call_splits(shp)
+    same = [i for i, s in enumerate(shp) if call_splits([s])[0] == call[i]]
+    print(f"alone: {len(same)} of {len(shp)} matrices split as in the call", flush=True)
+    assert len(same) >= len(shp) - 4
+    for i in same:
+        single = torch.empty_like(outs[i])
+        _lib.newton_schulz_into([(xs[i], single)], ns_coefficients=COEFFS)
+        assert torch.equal(outs[i], single), shp[i]
 
 
 def test_random_ragged_shapes_gram_form():

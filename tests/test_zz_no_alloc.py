@@ -36,8 +36,8 @@ def step(state, *, noalloc, lr, ns_form):
 @pytest.mark.parametrize("ns_form", ["standard", "gram"])
 def test_noalloc_matches_workspace_step_twice(ns_form):
     # large, ragged and small (short side <= 128) matrices, fp32 and bf16 params,
-    # so the first call runs several groups in the scratch; 2048 x 2048 runs
-    # every stage K-split (its partials in the scratch too), 1024 x 4096 its grams
+    # so the first call runs several groups in the scratch; the call splits its
+    # grams and the 2048 x 2048 symmetric products (partials in the scratch too)
     calls = [
         ([(1024, 4096), (700, 300), (96, 2000), (300, 1000), (2000, 64), (512, 512), (2048, 2048)], torch.float32),
         ([(256, 640), (100, 260)], torch.bfloat16),
