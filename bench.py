@@ -347,6 +347,8 @@ def main() -> int:
                          "production Newton-Schulz, the drop-in's default) after the standard-form timing")
     ap.add_argument("--cpu-budget", type=float, default=45.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-gpu", action="store_true",
+                    help="skip the stock torch.optim.Muon step on the GPU (reference_gpu)")
     ap.add_argument("--workspace-gib", type=float, default=0.0, help="libpanmuon workspace cap (0 = default)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, run a plain device copy of this many MiB 3x (HBM counter calibration)")
@@ -501,6 +503,41 @@ def main() -> int:
         print(f"bench: gram form {g_ms:.2f} ms/step", file=sys.stderr, flush=True)
         patch_muon(ns_form=args.ns_form)
 
+    # The reference's own PyTorch path on the same GPU and state, after the
+    # headline timing: stock torch.optim.Muon (torch's
+    # _zeropower_via_newtonschulz, one param at a time on hipBLASLt's bf16
+    # GEMMs, TORCH/optim/_muon.py:31-70) with a float lr, as the reference runs
+    # it without its patch (pan/optim/muon.py:126-128). Its momentum buffers
+    # are torch's own, zeros_like(grad) (torch's lerp takes no fp32 buffer with
+    # bf16 grads). Not for chunked groups, whose tuple adjust_lr_fn only the
+    # patched step takes.
+    ref_gpu = None
+    if not args.no_torch_gpu and not args.copy_mib and args.config not in CHUNKS:
+        ours = (torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon)
+        torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon = stock_fns
+        torch.cuda.empty_cache()
+        try:
+            ref_opt = torch.optim.Muon([{"params": params}], lr=0.02, weight_decay=0.01, momentum=0.95,
+                                       adjust_lr_fn="match_rms_adamw")
+            ref_opt.step()
+            torch.cuda.synchronize()
+            r_steps = min(args.steps, 2)
+            t0 = time.perf_counter()
+            for _ in range(r_steps):
+                ref_opt.step()
+            torch.cuda.synchronize()
+            r_ms = (time.perf_counter() - t0) * 1e3 / r_steps
+        finally:
+            torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon = ours
+        del ref_opt
+        torch.cuda.empty_cache()
+        ref_gpu = {"what": "stock torch.optim.Muon step on the same GPU, params and grads (torch's "
+                           "_zeropower_via_newtonschulz, one param at a time, hipBLASLt bf16 GEMMs, float lr, "
+                           "torch's own momentum buffers)",
+                   "ms_per_step": round(r_ms, 3), "value": round(f_ns / (r_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                   "steps": r_steps, "speedup": round(r_ms / ms_per_step, 3)}
+        print(f"bench: stock torch Muon on the GPU {r_ms:.2f} ms/step", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import baseline
@@ -555,6 +592,7 @@ def main() -> int:
         "hbm_stream": stream,
         "stages": stages,
         "gram_form": gram_form,
+        "reference_gpu": ref_gpu,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
