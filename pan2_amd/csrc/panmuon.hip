@@ -187,9 +187,13 @@ struct Item {
 // whose tiles fill the chip, the chunks' fp32 partials would cost more than
 // the idle CUs they fill (measured: 48 x 2048² runs 8.0 ms unsplit, 15.7 ms
 // split). The choice depends on the call only, so a call gives the same bits
-// in any workspace grouping and through either step entry point. GRAM
-// contracts over Np, the symmetric products and UPDATE / FINAL over Mp.
+// in any workspace grouping and through either step entry point. A matrix
+// whose partials would take its workspace past the allocation-free step's
+// scratch stays unsplit, so that step takes every matrix it would take
+// unsplit. GRAM contracts over Np, the symmetric products and UPDATE / FINAL
+// over Mp.
 void split_call(std::vector<Item>& items) {
+  constexpr size_t kTableRoom = 1u << 20;  // above any one-matrix descriptor table
   int64_t tiles[3] = {0, 0, 0};
   for (const Item& it : items)
     if (!it.plan.small) {
@@ -210,6 +214,10 @@ void split_call(std::vector<Item>& items) {
     if (p.ks_gram > 1) kp = std::max(kp, (size_t)sym_tiles(p) * p.ks_gram * tile_bytes);
     if (p.ks_symm > 1) kp = std::max(kp, (size_t)sym_tiles(p) * p.ks_symm * tile_bytes);
     if (p.ks_full > 1) kp = std::max(kp, (size_t)full_tiles(p) * p.ks_full * tile_bytes);
+    if (kp && p.ws + kp + kTableRoom > PM_NOALLOC_SCRATCH_BYTES) {
+      p.ks_gram = p.ks_symm = p.ks_full = 1;
+      kp = 0;
+    }
     p.kpart = kp;
     p.ws += kp;
   }

@@ -4,6 +4,9 @@ tests/native/tile_order_check.cpp pins the C++ itself) applied per call as
 pan2_amd/csrc/panmuon.hip::split_call does. A stage splits only when the
 call's engine matrices (short side > 128) together hold at most 128 of its
 tiles (two chunks) or 64 (four), and each matrix as far as its shape allows.
+(A matrix whose partials would take its workspace past the 256 MiB scratch of
+the allocation-free step also stays unsplit; no shape the tests give this
+restatement comes near that.)
 """
 
 

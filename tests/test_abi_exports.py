@@ -309,6 +309,20 @@ def test_k_split_is_decided_per_call(lib):
     assert capped < one - kp + (1 << 20)
 
 
+def test_k_split_keeps_a_matrix_within_the_noalloc_scratch(lib):
+    """A lone 3584 x 6144 splits its grams and symmetric products 2 ways in the
+    standard form (105 tiles x 2 chunks x 256 KiB of partials); in the gram
+    form (five square buffers) those partials would take it past the
+    allocation-free step's 256 MiB scratch, so it stays unsplit there."""
+    m, n, kp = 3584, 6144, 105 * 2 * 256 * 1024
+    x, sq = m * n * 2, m * m * 2  # X and one square buffer, bf16
+    std = ws_bytes(lib, [mat(m, n)])
+    assert 2 * x + 2 * sq + kp <= std <= 2 * x + 2 * sq + kp + (1 << 20)
+    hp = hparams(ns_form="gram")
+    gram = lib.pm_workspace_bytes(arr(mat(m, n)), 1, ctypes.byref(hp))
+    assert 2 * x + 5 * sq <= gram <= 2 * x + 5 * sq + (1 << 20) <= _lib.NOALLOC_SCRATCH_BYTES
+
+
 def test_gram_form_workspace_sizing(lib):
     M, N = 1024, 4096
     std = ws_bytes(lib, [mat(M, N)])
