@@ -86,6 +86,20 @@ def test_noalloc_rejects_a_matrix_beyond_the_scratch_untouched():
         assert torch.equal(a, b)
 
 
+def test_noalloc_takes_a_matrix_that_fits_unsplit():
+    """A lone 3584 x 6144 in the gram form fits the scratch unsplit (206 MiB);
+    its K-split partials would not, so the call does not split it, and the
+    scratch step equals the workspace step."""
+    shapes = [(3584, 6144)]
+    lr = torch.tensor(0.02, device=DEV)
+    ref = make_state(shapes, 900, torch.bfloat16)
+    got = make_state(shapes, 900, torch.bfloat16)
+    step(ref, noalloc=False, lr=lr, ns_form="gram")
+    step(got, noalloc=True, lr=lr, ns_form="gram")
+    torch.cuda.synchronize()
+    assert torch.equal(got[0][0], ref[0][0]) and torch.equal(got[2][0], ref[2][0])
+
+
 def test_noalloc_allocates_nothing_through_torch():
     """The call takes no memory from torch's caching allocator (the scratch is
     the library's static array)."""
