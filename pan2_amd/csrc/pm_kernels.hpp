@@ -1254,67 +1254,78 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
   // wide one it is turned across each 4-lane group (quad_transpose, every lane
   // active) so that it is too. Loads and stores are 8-byte (bf16) or 16-byte
   // (fp32) vectors where the param's row stride and base allow, else per
-  // element.
+  // element. The a·X term comes as full-line loads of X's rows, turned into
+  // quads through the staging slot (every lane active) before any lane leaves
+  // the band for the param's edge.
   const int vec_align = f32p ? 16 : 8;
   const bool vec = (ldp % 4 == 0) && ((uintptr_t)d.param % vec_align == 0);
   typedef typename PickVec<f32p>::type PV;
   typedef typename PickVec<f32p>::elem E;
   const int qbase_w = job.tj * kTile + (wave & 3) * kWaveCols + 4 * ((lane & 15) >> 2);  // wide: first column
+  const int xw_p = job.ti * kTile + (wave >> 2) * kWaveRows, xw_q = job.tj * kTile + (wave & 3) * kWaveCols;
 #pragma unroll
-  for (int mi = 0; mi < kMi; ++mi) {
-    __builtin_amdgcn_sched_barrier(0);
+  for (int hb = 0; hb < 2; ++hb) {
+    u32x4 xr[4][2];
+    if (ax && slot) load_rounds(xr, X, ldx, tx, xw_p + 64 * hb, xw_q, lane);
 #pragma unroll
-    for (int ni = 0; ni < kNi; ++ni) {
-      const int p0 = pbase + mi * 16, q = qbase + ni * 16;
-      u16x4 o;
+    for (int m = 0; m < 4; ++m) {
+      const int mi = 4 * hb + m;
+      __builtin_amdgcn_sched_barrier(0);
+      u16x4 xq[kNi] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+      if (ax && slot) unstage_band(slot, xr[m], xq, lane);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x = ax ? bf2f(X[ws_off(p0 + e, q, ldx, tx)]) : 0.0f;
-        o[e] = AX_IN_ACC ? f2bf(acc[mi][ni][e] * s) : f2bf((ca * x + acc[mi][ni][e]) * s);  // bf16 update
-      }
-      // param row r, columns c0 .. c0+3
-      int r = q, c0 = p0;
-      if (!tall) {
-        o = quad_transpose(o, lane);
-        r = pbase + mi * 16 + (lane & 3);  // pbase carries the lane's 4·(lane/16)
-        c0 = qbase_w + ni * 16;
-      }
-      if (r >= prow) continue;
-      const E* src = (const E*)d.param + (int64_t)r * ldp + c0;
-      PV pv{};
-      if (step) {
-        if (vec && c0 + 3 < pcol) {
-          pv = *(const PV*)src;
-        } else {
+      for (int ni = 0; ni < kNi; ++ni) {
+        const int p0 = pbase + mi * 16, q = qbase + ni * 16;
+        u16x4 o;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) pv[e] = c0 + e < pcol ? src[e] : (E)0;
+        for (int e = 0; e < 4; ++e) {
+          const float x = !ax ? 0.0f : slot ? bf2f(xq[ni][e]) : bf2f(X[ws_off(p0 + e, q, ldx, tx)]);
+          o[e] = AX_IN_ACC ? f2bf(acc[mi][ni][e] * s) : f2bf((ca * x + acc[mi][ni][e]) * s);  // bf16 update
         }
-      }
-      float out[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float on = bf2f(o[e]);
-        const float pe = f32p ? (float)pv[e] : bf2f((uint16_t)pv[e]);
-        out[e] = step ? pe * wdf + on * neg : on;
-      }
-      const bool full = vec && c0 + 3 < pcol;
-      if (f32p) {
-        float* dst = (float*)d.param + (int64_t)r * ldp + c0;
-        if (full) {
-          *(f32x4*)dst = (f32x4){out[0], out[1], out[2], out[3]};
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (c0 + e < pcol) dst[e] = out[e];
+        // param row r, columns c0 .. c0+3
+        int r = q, c0 = p0;
+        if (!tall) {
+          o = quad_transpose(o, lane);
+          r = pbase + mi * 16 + (lane & 3);  // pbase carries the lane's 4·(lane/16)
+          c0 = qbase_w + ni * 16;
         }
-      } else {
-        uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
-        if (full) {
-          *(u16x4*)dst = (u16x4){f2bf(out[0]), f2bf(out[1]), f2bf(out[2]), f2bf(out[3])};
-        } else {
+        if (r >= prow) continue;
+        const E* src = (const E*)d.param + (int64_t)r * ldp + c0;
+        PV pv{};
+        if (step) {
+          if (vec && c0 + 3 < pcol) {
+            pv = *(const PV*)src;
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (c0 + e < pcol) dst[e] = f2bf(out[e]);
+            for (int e = 0; e < 4; ++e) pv[e] = c0 + e < pcol ? src[e] : (E)0;
+          }
+        }
+        float out[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float on = bf2f(o[e]);
+          const float pe = f32p ? (float)pv[e] : bf2f((uint16_t)pv[e]);
+          out[e] = step ? pe * wdf + on * neg : on;
+        }
+        const bool full = vec && c0 + 3 < pcol;
+        if (f32p) {
+          float* dst = (float*)d.param + (int64_t)r * ldp + c0;
+          if (full) {
+            *(f32x4*)dst = (f32x4){out[0], out[1], out[2], out[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (c0 + e < pcol) dst[e] = out[e];
+          }
+        } else {
+          uint16_t* dst = (uint16_t*)d.param + (int64_t)r * ldp + c0;
+          if (full) {
+            *(u16x4*)dst = (u16x4){f2bf(out[0]), f2bf(out[1]), f2bf(out[2]), f2bf(out[3])};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (c0 + e < pcol) dst[e] = f2bf(out[e]);
+          }
         }
       }
     }
