@@ -1249,7 +1249,135 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
       return;
     }
   }
-  // Element path (fp32 params, and tiles at a param's edge): quad by quad. A
+  if (f32p && slot && step) {
+    // fp32 params: the same full-line path as bf16 params, each 8-element run
+    // of a param row read and written as two 16-byte vectors. Two bands (wide)
+    // or two 16-column blocks (tall) at a time, so the param values held in
+    // registers stay within budget.
+    const int pw = job.ti * kTile + (wave >> 2) * kWaveRows, qw = job.tj * kTile + (wave & 3) * kWaveCols;
+    const bool inside = tall ? (qw + kWaveCols <= prow && pw + kWaveRows <= pcol)
+                             : (pw + kWaveRows <= prow && qw + kWaveCols <= pcol);
+    const bool whole = inside && ldp % 8 == 0 && (uintptr_t)d.param % 16 == 0;
+    float* P = (float*)d.param;
+    // p <- p·(1 - lr·wd) - lr·adj·O for the 8 elements of O's 16-byte run `on`
+    // and the param run p0, p1 at dst (the element path's fp32 operations)
+    auto step8f = [&](const u32x4& on, const f32x4& p0, const f32x4& p1, float* dst) {
+      f32x4 r0, r1;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float lo = bf2f((uint16_t)(on[k] & 0xffffu)), hi = bf2f((uint16_t)(on[k] >> 16));
+        const float plo = k < 2 ? p0[2 * k] : p1[2 * k - 4], phi = k < 2 ? p0[2 * k + 1] : p1[2 * k - 3];
+        const float olo = plo * wdf + lo * neg, ohi = phi * wdf + hi * neg;
+        if (k < 2) {
+          r0[2 * k] = olo;
+          r0[2 * k + 1] = ohi;
+        } else {
+          r1[2 * k - 4] = olo;
+          r1[2 * k - 3] = ohi;
+        }
+      }
+      *(f32x4*)dst = r0;
+      *(f32x4*)(dst + 4) = r1;
+    };
+    if (whole && !tall) {
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 xr[4][2];
+        if (ax) load_rounds(xr, X, ldx, tx, pw + 64 * hb, qw, lane);
+#pragma unroll
+        for (int mh = 0; mh < 2; ++mh) {
+          f32x4 pv[2][2][2];
+#pragma unroll
+          for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float* row =
+                  P + (int64_t)(pw + 64 * hb + 16 * (2 * mh + m2) + 8 * h + (lane >> 3)) * ldp + qw + 8 * (lane & 7);
+              pv[m2][h][0] = *(const f32x4*)row;
+              pv[m2][h][1] = *(const f32x4*)(row + 4);
+            }
+#pragma unroll
+          for (int m2 = 0; m2 < 2; ++m2) {
+            const int m = 2 * mh + m2;
+            u16x4 xq[kNi] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+            if (ax) unstage_band(slot, xr[m], xq, lane);
+            u16x4 o[kNi];
+#pragma unroll
+            for (int ni = 0; ni < kNi; ++ni)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float a = acc[4 * hb + m][ni][e];
+                o[ni][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xq[ni][e]) + a) * s);  // bf16 update
+              }
+            stage_band(slot, o, lane);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int r = 8 * h + (lane >> 3), c = lane & 7;
+              const u32x4 on = *(const u32x4*)(slot + r * 128 + ((c ^ swz_norm(r)) << 4));
+              step8f(on, pv[m2][h][0], pv[m2][h][1], P + (int64_t)(pw + 64 * hb + 16 * m + r) * ldp + qw + 8 * c);
+            }
+          }
+        }
+      }
+      return;
+    }
+    if (whole) {
+      // tall: as for bf16 params, each 16-column block of C (16 param rows)
+      // staged transposed
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        __builtin_amdgcn_sched_barrier(0);
+        u16x4 xb[4][kNi];
+        const int xrow = pw + 64 * hb + 4 * (lane >> 4) + (lane & 3), xcol = qw + 4 * ((lane & 15) >> 2);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int ni = 0; ni < kNi; ++ni)
+            xb[m][ni] = ax ? *(const u16x4*)(X + ws_off(xrow + 16 * m, xcol + 16 * ni, ldx, tx)) : (u16x4){0, 0, 0, 0};
+        if (ax) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int ni = 0; ni < kNi; ++ni) xb[m][ni] = quad_transpose(xb[m][ni], lane);
+        }
+#pragma unroll
+        for (int nh = 0; nh < 2; ++nh) {
+          f32x4 pv[2][2][2];
+#pragma unroll
+          for (int n2 = 0; n2 < 2; ++n2)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float* row =
+                  P + (int64_t)(qw + 16 * (2 * nh + n2) + 8 * h + (lane >> 3)) * ldp + pw + 64 * hb + 8 * (lane & 7);
+              pv[n2][h][0] = *(const f32x4*)row;
+              pv[n2][h][1] = *(const f32x4*)(row + 4);
+            }
+#pragma unroll
+          for (int n2 = 0; n2 < 2; ++n2) {
+            const int ni = 2 * nh + n2;
+            u16x4 blk[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float a = acc[4 * hb + m][ni][e];
+                blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xb[m][ni][e]) + a) * s);  // bf16 update
+              }
+            stage_block_tr(slot, blk, lane);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int r = 8 * h + (lane >> 3), c = lane & 7;
+              const u32x4 on = *(const u32x4*)(slot + r * 128 + ((c ^ swz_tr(r)) << 4));
+              step8f(on, pv[n2][h][0], pv[n2][h][1], P + (int64_t)(qw + 16 * ni + r) * ldp + pw + 64 * hb + 8 * c);
+            }
+          }
+        }
+      }
+      return;
+    }
+  }
+  // Element path (tiles at a param's edge, unaligned params): quad by quad. A
   // quad is 4 consecutive elements of one param row for a tall param; for a
   // wide one it is turned across each 4-lane group (quad_transpose, every lane
   // active) so that it is too. Loads and stores are 8-byte (bf16) or 16-byte
