@@ -107,6 +107,8 @@ def _single_tensor_muon(
             assert R % total_chunks == 0, "# rows must be divisible by # local chunks (chunks must be same-shape)"
         if not param.is_cuda:
             raise RuntimeError("pan2_amd Muon runs on HIP device tensors only; got a CPU parameter")
+        if param.numel() == 0:
+            continue  # torch's step leaves an empty param and its buffer as they are
         p_list.append(param)
         g_list.append(grad)
         b_list.append(buf)
@@ -146,6 +148,8 @@ def newton_schulz(grad: Tensor, ns_coefficients, ns_steps: int, eps: float) -> T
     x = grad if grad.dtype in (torch.float32, torch.bfloat16) else grad.float()
     x = x.contiguous()
     out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    if out.numel() == 0:
+        return out  # torch's NS returns an empty matrix unchanged in shape
     flat_in = x.reshape(-1, *x.shape[-2:])
     flat_out = out.view(-1, *x.shape[-2:])
     _lib.newton_schulz_into([(flat_in[i], flat_out[i]) for i in range(flat_in.shape[0])],

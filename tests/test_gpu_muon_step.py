@@ -150,6 +150,25 @@ def test_grad_none_skipped_and_zero_grad(patched):
     assert torch.equal(a.detach().cpu(), (a0.cpu() * torch.tensor(wdf)))
 
 
+def test_empty_param_is_left_alone(patched):
+    """An empty 2-D param steps as in torch (TORCH/optim/_muon.py:31-70 and
+    :290-320 leave it as it is): no error, the other params of the group
+    step as they would without it, and the NS of an empty matrix is empty."""
+    a = torch.nn.Parameter(cpu_rand((256, 512), 5, 0.02).to(DEV))
+    e = torch.nn.Parameter(torch.zeros((0, 128), device=DEV))
+    twin = torch.nn.Parameter(a.detach().clone())
+    for p in (a, twin):
+        p.grad = cpu_rand((256, 512), 6, 1e-3).to(DEV)
+    e.grad = torch.zeros_like(e)
+    torch.optim.Muon([a, e], lr=torch.tensor(0.02, device=DEV), weight_decay=0.01).step()
+    torch.optim.Muon([twin], lr=torch.tensor(0.02, device=DEV), weight_decay=0.01).step()
+    torch.cuda.synchronize()
+    assert e.shape == (0, 128)
+    assert torch.equal(a.detach(), twin.detach())
+    out = torch_muon._zeropower_via_newtonschulz(torch.zeros((0, 64), device=DEV), (3.4445, -4.7750, 2.0315), 5, 1e-7)
+    assert out.shape == (0, 64) and out.dtype == torch.bfloat16
+
+
 def test_nan_grad_propagates(patched):
     p = torch.nn.Parameter(cpu_rand((256, 512), 4, 0.02).to(DEV))
     g = cpu_rand((256, 512), 5, 1e-3)
