@@ -949,10 +949,8 @@ __device__ __forceinline__ int xcc_id() {
 // to bf16 where torch rounds it.
 // PDT is the param dtype of the FINAL epilogue (one instantiation per dtype
 // keeps the epilogue's registers within budget); other stages ignore it.
-// AX_IN_ACC (FINAL): the caller has already added a·X to the accumulators
-// (acc = a·x + acc, the same fp32 operations), so X is not read again.
-// slot: this wave's staging slot (kStageBytes of LDS) for GRAM, SYMM and UPDATE.
-template <int STAGE, int PDT, int LAYOUT, bool AX_IN_ACC = false, class D>
+// slot: this wave's staging slot (kStageBytes of LDS).
+template <int STAGE, int PDT, int LAYOUT, class D>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, const TileJob& job,
                                               const f32x4 (&acc)[kMi][kNi], int wave, char* slot = nullptr) {
 #pragma clang fp contract(off)
@@ -1130,7 +1128,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
     }
   }
   const bool step = args.mode == MODE_STEP;
-  const bool ax = !AX_IN_ACC && ca != 0.0f;
+  const bool ax = ca != 0.0f;
   constexpr bool f32p = PDT == DT_F32;  // MODE_NS launches the bf16 instantiation
   // param update of 8 consecutive bf16 elements (one 16-byte run)
   auto step8 = [&](const u32x4& on, const u32x4& pv) {
@@ -1184,7 +1182,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float a = acc[4 * hb + m][ni][e];
-              o[ni][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xq[ni][e]) + a) * s);  // bf16 update
+              o[ni][e] = f2bf((ca * bf2f(xq[ni][e]) + a) * s);  // bf16 update
             }
           stage_band(slot, o, lane);
 #pragma unroll
@@ -1235,7 +1233,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float a = acc[4 * hb + m][ni][e];
-              blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xb[m][ni][e]) + a) * s);  // bf16 update
+              blk[m][e] = f2bf((ca * bf2f(xb[m][ni][e]) + a) * s);  // bf16 update
             }
           stage_block_tr(slot, blk, lane);
 #pragma unroll
@@ -1308,7 +1306,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const float a = acc[4 * hb + m][ni][e];
-                o[ni][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xq[ni][e]) + a) * s);  // bf16 update
+                o[ni][e] = f2bf((ca * bf2f(xq[ni][e]) + a) * s);  // bf16 update
               }
             stage_band(slot, o, lane);
 #pragma unroll
@@ -1362,7 +1360,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const float a = acc[4 * hb + m][ni][e];
-                blk[m][e] = AX_IN_ACC ? f2bf(a * s) : f2bf((ca * bf2f(xb[m][ni][e]) + a) * s);  // bf16 update
+                blk[m][e] = f2bf((ca * bf2f(xb[m][ni][e]) + a) * s);  // bf16 update
               }
             stage_block_tr(slot, blk, lane);
 #pragma unroll
@@ -1408,7 +1406,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float x = !ax ? 0.0f : slot ? bf2f(xq[ni][e]) : bf2f(X[ws_off(p0 + e, q, ldx, tx)]);
-          o[e] = AX_IN_ACC ? f2bf(acc[mi][ni][e] * s) : f2bf((ca * x + acc[mi][ni][e]) * s);  // bf16 update
+          o[e] = f2bf((ca * x + acc[mi][ni][e]) * s);  // bf16 update
         }
         // param row r, columns c0 .. c0+3
         int r = q, c0 = p0;
