@@ -116,3 +116,44 @@ def test_random_ragged_shapes_gram_form():
         _lib.newton_schulz_into([(x, o)], ns_coefficients=COEFFS, ns_form="gram")
     for s, o, o1 in zip(shp, outs, singles):
         assert torch.equal(o, o1), s
+
+
+@pytest.mark.parametrize("form", ["standard", "gram"])
+def test_random_mid_size_calls_split_or_not(form):
+    """Seeded random calls of mid-size matrices (short sides 400-2100, long
+    sides up to 6000), small ones beside them, some calls small enough to
+    K-split (tests/ksplit_rule.py), some not: each call gives the same bits in
+    one workspace group and in several, each matrix alone gives the same bits
+    wherever its split is the call's, and the standard form stays within the
+    gate against the float32 NS on the GPU (max(2e-2, 1.25 x torch's own bf16
+    NS on the GPU, TORCH/optim/_muon.py:31-70))."""
+    from tests.conftest import TORCH_ZEROPOWER
+
+    rng = np.random.default_rng(4321 if form == "standard" else 8765)
+    for call in range(3):
+        n = int(rng.integers(1, 6))
+        shp = []
+        for _ in range(n):
+            short, long = int(rng.integers(400, 2101)), int(rng.integers(2100, 6001))
+            shp.append((short, long) if rng.integers(0, 2) == 0 else (long, short))
+        if call == 1:
+            shp.append((96, 3000))  # a small matrix in the same call
+        splits = call_splits(shp)
+        print(f"{form} call {call}: {shp} chunks {splits}", flush=True)
+        gen = torch.Generator(device=DEV).manual_seed(100 + call)
+        xs = [torch.randn(s, generator=gen, device=DEV, dtype=torch.float32) for s in shp]
+        one = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shp]
+        many = [torch.empty(s, dtype=torch.bfloat16, device=DEV) for s in shp]
+        _lib.newton_schulz_into(list(zip(xs, one)), ns_coefficients=COEFFS, ns_form=form)
+        _lib.newton_schulz_into(list(zip(xs, many)), ns_coefficients=COEFFS, ns_form=form, workspace_limit=1)
+        for i, s in enumerate(shp):
+            assert torch.equal(one[i], many[i]), (s, "workspace groups")
+            if call_splits([s])[0] == splits[i]:
+                alone = torch.empty(s, dtype=torch.bfloat16, device=DEV)
+                _lib.newton_schulz_into([(xs[i], alone)], ns_coefficients=COEFFS, ns_form=form)
+                assert torch.equal(alone, one[i]), (s, "alone")
+            if form == "standard":
+                ref = ns_fp32(xs[i]).double()
+                err = float((one[i].double() - ref).norm() / ref.norm())
+                err_t = float((TORCH_ZEROPOWER(xs[i], COEFFS, 5, 1e-7).double() - ref).norm() / ref.norm())
+                assert err <= max(2e-2, 1.25 * err_t), (s, err, err_t)
