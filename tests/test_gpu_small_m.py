@@ -350,3 +350,24 @@ def test_many_small_muon_steps_fused_equal_single(ns_form, dtypes):
         _lib.muon_step([p1], [g0[i]], [b1], [1.0], **kw)
         assert torch.equal(bs[i], b1), ("momentum", i, shapes[i])
         assert torch.equal(ps[i], p1), ("param", i, shapes[i])
+
+
+@pytest.mark.parametrize("steps", [2, 5])
+def test_batched_gram_newtonschulz_drop_in(steps):
+    """pan/optim/muon_triton.py:303-345's public pair on the device: the
+    predicate's answer, and batched_gram_newtonschulz over [100, 128, N]
+    equal bit for bit to the library's gram form on the same matrices, the
+    result in X's own storage when the batch resets (ns_steps > 2), in a new
+    tensor otherwise, as in the reference."""
+    from pan2_amd.optim.kernels import batched_gram_newtonschulz, can_use_fused_gram_ns
+
+    x = torch.stack([seeded((128, 640), 7000 + i) for i in range(100)]).to(DEV).bfloat16()
+    assert can_use_fused_gram_ns(x) and not can_use_fused_gram_ns(x[:95])
+    want = [torch.empty((128, 640), dtype=torch.bfloat16, device=DEV) for _ in range(100)]
+    _lib.newton_schulz_into([(x[i], want[i]) for i in range(100)], ns_steps=steps, ns_form="gram")
+    ptr = x.data_ptr()
+    got = batched_gram_newtonschulz(x, (3.4445, -4.7750, 2.0315), steps, 1e-7)
+    torch.cuda.synchronize()
+    assert (got.data_ptr() == ptr) == (steps > 2)
+    for i in range(100):
+        assert torch.equal(got[i], want[i]), i

@@ -265,3 +265,22 @@ def test_adam_descriptor_pass_layout_and_statuses():
     with pytest.raises(RuntimeError, match="differ in length"):
         h.fill_adam(arr.ctypes.data, ps, gs[:-1], ms, vs, [], st, hip_only=False)
     assert h.fill_adam(0, [], [], [], [], [], []) == h.FILLED
+
+
+def test_fused_gram_ns_predicate_and_reset_sets():
+    """pan/optim/muon_triton.py:303-345's public pair, on the host: the
+    predicate keeps the reference's answer, and reset sets the library's gram
+    form does not run raise before anything else."""
+    from pan2_amd.optim.kernels import batched_gram_newtonschulz, can_use_fused_gram_ns
+
+    assert not can_use_fused_gram_ns(torch.zeros(96, 128, 256))  # a CPU tensor
+    assert not can_use_fused_gram_ns(torch.zeros(128, 256)) and not can_use_fused_gram_ns(None)
+    x = torch.zeros(4, 128, 256)
+    with pytest.raises(ValueError, match="iteration 2"):
+        batched_gram_newtonschulz(x, (3.4445, -4.7750, 2.0315), 5, 1e-7, reset_iterations=frozenset([3]))
+    with pytest.raises(ValueError, match="iteration 2"):
+        batched_gram_newtonschulz(x, (3.4445, -4.7750, 2.0315), 5, 1e-7, reset_iterations=frozenset())
+    with pytest.raises(ValueError, match="does not reset"):
+        batched_gram_newtonschulz(x, (3.4445, -4.7750, 2.0315), 2, 1e-7, reset_iterations=frozenset([1]))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        batched_gram_newtonschulz(x, (3.4445, -4.7750, 2.0315), 5, 1e-7)
