@@ -523,15 +523,13 @@ def adam_dtype_code(t: torch.Tensor) -> int:
 
 def adam_descs(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps):
     """The pm_adam_tensor array of one call, filled in one C++ pass, or None
-    when some tensor is off params[0]'s HIP device or of a dtype pm_adam_step
+    when some tensor is off params[0]'s HIP device, of a dtype pm_adam_step
     does not take (float32 / bfloat16 / float16; max_exp_avg_sq of
-    exp_avg_sq's dtype; float32 steps). max_exp_avg_sqs: [] without amsgrad.
-    Raises ValueError for a grad that is not contiguous."""
+    exp_avg_sq's dtype; float32 steps), not contiguous, or of another element
+    count than its param. max_exp_avg_sqs: [] without amsgrad."""
     h = host_ext()
     arr = np.empty(len(params), dtype=_PM_ADAM_NP)
     rc = h.fill_adam(arr.ctypes.data, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps)
-    if rc == h.GRAD_NOT_CONTIGUOUS:
-        raise ValueError("grads must be contiguous")
     return arr if rc == h.FILLED else None
 
 
@@ -561,9 +559,9 @@ def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps
     in place, steps included). lr: float, or a 1-element tensor (read on the
     device when it lives there). max_exp_avg_sqs: read with amsgrad only.
     trusted: the lists come from torch's Adam, whose _init_group already
-    guarantees one device, matching shapes, contiguous state and float32
-    device steps; the descriptor pass still checks devices, dtypes and the
-    grads' contiguity."""
+    guarantees one device, matching shapes and float32 device steps; the
+    descriptor pass still checks devices, dtypes, element counts and
+    contiguity."""
     n = len(params)
     if n == 0:
         return
@@ -574,8 +572,8 @@ def adam_step(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps
         _check_adam_lists(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, dev)
     arr = adam_descs(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs if amsgrad else [], state_steps)
     if arr is None:
-        raise ValueError("pm_adam_step takes float32 / bfloat16 / float16 tensors on one HIP device, "
-                         "max_exp_avg_sq of exp_avg_sq's dtype and float32 steps")
+        raise ValueError("pm_adam_step takes contiguous float32 / bfloat16 / float16 tensors of their param's "
+                         "size on one HIP device, max_exp_avg_sq of exp_avg_sq's dtype and float32 steps")
     adam_launch(arr, dev, lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
                 maximize=maximize, decoupled=decoupled, grad_scale=grad_scale, found_inf=found_inf)
 

@@ -27,18 +27,19 @@ int32_t dtype_code(c10::ScalarType s) {
 }
 
 // Status of fill_adam.
-enum FillStatus : int { kFilled = 0, kGeneral = 1, kGradNotContiguous = 2 };
+enum FillStatus : int { kFilled = 0, kGeneral = 1 };
 
 // Fills the n-entry pm_adam_tensor array at address `out` from the lists of
 // one fused-Adam call (max_exp_avg_sqs empty without amsgrad). Returns
 // kFilled when every tensor is on params[0]'s HIP device with a dtype
-// pm_adam_step takes (max_exp_avg_sq of exp_avg_sq's dtype, steps float32)
-// and every grad is contiguous. kGeneral: some tensor is on another device or
-// of another dtype (the caller's general path splits the lists);
-// kGradNotContiguous: a grad is not contiguous. The array is complete only on
-// kFilled. List lengths that differ raise. hip_only = false also fills from
-// CPU tensors, for the CPU tests of the array's layout (pm_adam_step needs
-// device pointers: the product path keeps the default).
+// pm_adam_step takes (max_exp_avg_sq of exp_avg_sq's dtype, steps float32),
+// and every param, grad and state tensor is contiguous with its param's
+// element count: pm_adam_step walks the five as flat arrays of one length,
+// which is right only when their memory orders agree. kGeneral otherwise
+// (the caller's general path splits the lists); the array is complete only
+// on kFilled. List lengths that differ raise. hip_only = false also fills
+// from CPU tensors, for the CPU tests of the array's layout (pm_adam_step
+// needs device pointers: the product path keeps the default).
 int fill_adam(int64_t out, const std::vector<at::Tensor>& params, const std::vector<at::Tensor>& grads,
               const std::vector<at::Tensor>& exp_avgs, const std::vector<at::Tensor>& exp_avg_sqs,
               const std::vector<at::Tensor>& max_exp_avg_sqs, const std::vector<at::Tensor>& steps,
@@ -61,16 +62,20 @@ int fill_adam(int64_t out, const std::vector<at::Tensor>& params, const std::vec
     const at::Tensor& s = steps[i];
     if (p.device() != dev || g.device() != dev || m.device() != dev || v.device() != dev || s.device() != dev)
       return kGeneral;
+    const int64_t numel = p.numel();
+    if (!p.is_contiguous() || !g.is_contiguous() || !m.is_contiguous() || !v.is_contiguous() ||
+        g.numel() != numel || m.numel() != numel || v.numel() != numel || s.numel() != 1)
+      return kGeneral;
     const int32_t cp = dtype_code(p.scalar_type()), cg = dtype_code(g.scalar_type());
     const int32_t cm = dtype_code(m.scalar_type()), cv = dtype_code(v.scalar_type());
     if (cp < 0 || cg < 0 || cm < 0 || cv < 0 || s.scalar_type() != c10::ScalarType::Float) return kGeneral;
     void* x = nullptr;
     if (amsgrad) {
       const at::Tensor& t = max_exp_avg_sqs[i];
-      if (t.device() != dev || t.scalar_type() != v.scalar_type()) return kGeneral;
+      if (t.device() != dev || t.scalar_type() != v.scalar_type() || !t.is_contiguous() || t.numel() != numel)
+        return kGeneral;
       x = t.data_ptr();
     }
-    if (!g.is_contiguous()) return kGradNotContiguous;
     pm_adam_tensor& e = d[i];
     e.param = p.data_ptr();
     e.grad = g.data_ptr();
@@ -78,7 +83,7 @@ int fill_adam(int64_t out, const std::vector<at::Tensor>& params, const std::vec
     e.exp_avg_sq = v.data_ptr();
     e.max_exp_avg_sq = x;
     e.step = static_cast<float*>(s.data_ptr());
-    e.numel = p.numel();
+    e.numel = numel;
     e.param_dtype = cp;
     e.grad_dtype = cg;
     e.exp_avg_dtype = cm;
@@ -96,6 +101,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("max_exp_avg_sqs"), pybind11::arg("steps"), pybind11::arg("hip_only") = true);
   m.attr("FILLED") = static_cast<int>(kFilled);
   m.attr("GENERAL") = static_cast<int>(kGeneral);
-  m.attr("GRAD_NOT_CONTIGUOUS") = static_cast<int>(kGradNotContiguous);
   m.attr("DESC_BYTES") = static_cast<int>(sizeof(pm_adam_tensor));
 }

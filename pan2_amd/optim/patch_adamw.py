@@ -12,10 +12,10 @@ stream, with no host synchronisation. The optimizer object, its param groups
 and its state (``step``, ``exp_avg``, ``exp_avg_sq``) stay torch's, so
 state_dict and checkpoints are unchanged.
 
-Tensors the library does not take (float64, complex, or on the CPU) go to
-torch's own fused Adam, saved when this module is imported, exactly as an
-unpatched process would run them; fp32, bf16 and fp16 device tensors go to
-``pm_adam_step``.
+Tensors the library does not take (float64, complex, on the CPU, or not
+contiguous) go to torch's own fused Adam, saved when this module is imported,
+exactly as an unpatched process would run them; contiguous fp32, bf16 and fp16
+device tensors go to ``pm_adam_step``.
 """
 from __future__ import annotations
 
@@ -38,9 +38,11 @@ def _scalar(x):
 
 
 def _native(i, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, amsgrad) -> bool:
-    """Does pm_adam_step take tensor i: real fp32 / bf16 / fp16 device tensors throughout?"""
+    """Does pm_adam_step take tensor i: contiguous fp32 / bf16 / fp16 device
+    tensors of the param's size throughout? (It walks them as flat arrays.)"""
     ts = [params[i], grads[i], exp_avgs[i], exp_avg_sqs[i]] + ([max_exp_avg_sqs[i]] if amsgrad else [])
-    return all(t.is_cuda and t.dtype in _lib.ADAM_DTYPES for t in ts)
+    n = params[i].numel()
+    return all(t.is_cuda and t.dtype in _lib.ADAM_DTYPES and t.is_contiguous() and t.numel() == n for t in ts)
 
 
 @torch.compiler.disable

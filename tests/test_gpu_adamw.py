@@ -268,6 +268,40 @@ def test_unsupported_tensors_go_to_torchs_fused_adam(torch_fused_adam):
     assert torch.all((p_t - p_o).abs() <= 2e-6 * p_t.abs() + 1e-9)
 
 
+def test_noncontiguous_tensors_go_to_torchs_fused_adam(torch_fused_adam):
+    """A transposed param (its state and grad of the same strides, as torch's
+    zeros_like and autograd make them) is not walked as a flat array by
+    pm_adam_step: torch's own fused Adam steps it, bit for bit what an
+    unpatched process computes; the contiguous param of the same call still
+    runs on libpanmuon."""
+    from pan2_amd.optim import patch_adamw
+
+    kw = dict(amsgrad=True, has_complex=False, beta1=0.9, beta2=0.99, lr=1e-3, weight_decay=0.01, eps=1e-8,
+              maximize=False, capturable=False, differentiable=False, decoupled_weight_decay=True)
+    runs = []
+    for ours in (False, True):
+        gen = torch.Generator().manual_seed(17)
+        ps = [torch.randn(48, 64, generator=gen).to(DEV).t(), torch.randn(4096, generator=gen).to(DEV)]
+        assert not ps[0].is_contiguous()
+        ms, vs, xs = ([torch.zeros_like(p) for p in ps] for _ in range(3))
+        st = [torch.zeros((), device=DEV) for _ in ps]
+        for k in range(2):
+            gs = [(torch.randn(p.shape, generator=gen) * 1e-2).to(DEV) for p in ps]
+            gs[0] = torch.empty_like(ps[0]).copy_(gs[0])  # the param's strides, as autograd gives
+            if ours:
+                patch_adamw._fused_adam(ps, gs, ms, vs, xs, st, None, None, **kw)
+            else:
+                with torch_fused_adam():
+                    ADAM_MODULE._fused_adam(ps, gs, ms, vs, xs, st, None, None, **kw)
+        torch.cuda.synchronize()
+        runs.append([[t.cpu() for t in ts] for ts in (ps, ms, vs, xs)] + [[float(s) for s in st]])
+    for a, b in zip(runs[0][:4], runs[1][:4]):  # the transposed param: torch's kernel on both sides
+        assert torch.equal(a[0], b[0])
+    assert runs[0][4] == runs[1][4] == [2.0, 2.0]
+    p_t, p_o = runs[0][0][1], runs[1][0][1]
+    assert torch.all((p_t - p_o).abs() <= 2e-6 * p_t.abs() + 1e-9)
+
+
 def test_found_inf_skips_like_torch(torch_fused_adam):
     """A GradScaler's found_inf = 1 leaves params, moments and steps untouched; 0 steps normally."""
     for flag in (1.0, 0.0):

@@ -259,9 +259,25 @@ def test_adam_descriptor_pass_layout_and_statuses():
                 {"x": torch.zeros(ps[0].shape, dtype=torch.float64)}):
         p2, s2, x2 = [bad.get("p", ps[0])] + ps[1:], [bad.get("s", st[0])] + st[1:], [bad.get("x", xs[0])] + xs[1:]
         assert h.fill_adam(arr.ctypes.data, p2, gs, ms, vs, x2 if "x" in bad else [], s2, hip_only=False) == h.GENERAL
-    nc = [torch.zeros(4, 6)[:, ::2]] + gs[1:]
-    assert h.fill_adam(arr.ctypes.data, [torch.zeros(4, 3)] + ps[1:], nc, ms, vs, [], st,
-                       hip_only=False) == h.GRAD_NOT_CONTIGUOUS
+    # pm_adam_step walks the tensors as flat arrays of the param's length: a
+    # tensor that is not contiguous (here a strided grad, a transposed param
+    # with state of its strides, a strided max_exp_avg_sq) or of another
+    # element count goes to the general path
+    p43 = torch.zeros(4, 3)
+    assert h.fill_adam(arr.ctypes.data, [p43] + ps[1:], [torch.zeros(4, 6)[:, ::2]] + gs[1:], ms, vs, [], st,
+                       hip_only=False) == h.GENERAL
+    pt = torch.zeros(3, 4).t()
+    assert h.fill_adam(arr.ctypes.data, [pt] + ps[1:], [torch.zeros_like(pt)] + gs[1:], [torch.zeros_like(pt)] + ms[1:],
+                       [torch.zeros_like(pt)] + vs[1:], [], st, hip_only=False) == h.GENERAL
+    assert h.fill_adam(arr.ctypes.data, ps, gs, ms, vs, [torch.zeros(2 * ps[0].numel())[::2]] + xs[1:], st,
+                       hip_only=False) == h.GENERAL
+    for short in ("g", "m", "v", "x"):
+        t = torch.zeros(ps[0].numel() - 1, dtype=ps[0].dtype)
+        lists = {k: list(v) for k, v in (("g", gs), ("m", ms), ("v", vs), ("x", xs))}
+        lists[short][0] = t
+        assert h.fill_adam(arr.ctypes.data, ps, lists["g"], lists["m"], lists["v"], lists["x"], st,
+                           hip_only=False) == h.GENERAL, short
+    assert h.fill_adam(arr.ctypes.data, ps, gs, ms, vs, [], [torch.zeros(2)] + st[1:], hip_only=False) == h.GENERAL
     with pytest.raises(RuntimeError, match="differ in length"):
         h.fill_adam(arr.ctypes.data, ps, gs[:-1], ms, vs, [], st, hip_only=False)
     assert h.fill_adam(0, [], [], [], [], [], []) == h.FILLED
