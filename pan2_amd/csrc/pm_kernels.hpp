@@ -975,8 +975,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
     // SYMM stores its upper part and mirrors it, so every symmetric product
     // is exactly symmetric (later products read R and the addend through
     // their transposes). A GRAM diagonal tile is bitwise symmetric already
-    // (the same products in the same order), and so is SYMM's when L == R.
-    const bool diag = STAGE == ST_SYMM && !mirror;
+    // (the same products in the same order), and so is SYMM's when L == R
+    // (the standard form's A·A, the gram form's R·R): those go through the
+    // full-tile stores. SYMM's full tiles always store the mirror too; on such
+    // a diagonal tile it writes every element again with the same bits.
+    const bool diag = STAGE == ST_SYMM && !mirror && args.sl != args.sr;
     if (ts && !diag) {
       // full tiles: staged full-line stores, normal orientation and (off the
       // diagonal) the mirror, band group by band group; the addend (symmetric,
@@ -1013,7 +1016,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const D& d, 
           const int p0 = pw + (4 * hb + m) * 16;
           stage_flush<false>(slot, lane, C + ws_off(p0, qw, ldc, ts), ts ? 64 : (int)ldc);
         }
-        if (mirror) {
+        if (STAGE == ST_SYMM || mirror) {
 #pragma unroll
           for (int ni = 0; ni < kNi; ++ni) {
             const u16x4 blk[4] = {o[0][ni], o[1][ni], o[2][ni], o[3][ni]};
