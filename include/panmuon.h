@@ -155,6 +155,10 @@ size_t pm_workspace_bytes(const pm_matrix* mats, int n, const pm_hparams* hp);
  *                                    (pan/optim/muon_triton.py:130-131,188-190)
  * lr is read from lr_dev (a device float, the reference's tensor lr path,
  * pan/optim/muon_triton.py:152-159) when it is not NULL, else lr_host.
+ * On a stream under graph capture the descriptor table goes in as kernel
+ * arguments rather than as a copy from the library's staging buffers, so a
+ * captured call replays correctly while the workspace it was given stays
+ * allocated (the same holds for pm_newton_schulz and pm_adam_step).
  */
 int pm_muon_step(const pm_matrix* mats, int n, const pm_hparams* hp,
                  const float* lr_dev, double lr_host,

@@ -223,9 +223,14 @@ void split_call(std::vector<Item>& items) {
   }
 }
 
+int load_table_by_kernel(const char* src, size_t bytes, char* dst, hipStream_t stream);
+
 // Descriptor uploads go through pinned staging buffers: the host table is
 // copied into one, and an asynchronous copy on the caller's stream moves it
-// to the workspace, so the host does not wait for the stream. A buffer is
+// to the workspace, so the host does not wait for the stream. On a stream
+// under graph capture the table goes in as kernel arguments instead
+// (load_table_by_kernel): a captured copy would read the staging buffer again
+// at every replay, after later calls have reused it. A buffer is
 // reused once the event recorded after its copy has completed (the smallest
 // free one that holds the table, else the largest free one, regrown). The
 // pool grows while every buffer is still in flight (calls queued far behind
@@ -249,8 +254,12 @@ std::vector<Staging> g_stage;
 uint64_t g_stage_seq = 0;
 
 int upload(const void* src, size_t bytes, void* dst, hipStream_t stream) {
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &capture);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (capture != hipStreamCaptureStatusNone) return load_table_by_kernel((const char*)src, bytes, (char*)dst, stream);
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_stage_mu);
   Staging* s = nullptr;
@@ -616,11 +625,10 @@ int run_small(Launcher& L, const pm_hparams* hp, bool fused, bool pro_gram) {
 // Runs one group: items[0, count) share the workspace `ws` and are all small
 // or all not.
 // How a group's descriptor table reaches the workspace: an asynchronous copy
-// from a pinned staging buffer (upload), or kernels that take it as by-value
-// arguments (load_table_by_kernel: no staging memory, for
-// pm_muon_step_noalloc).
+// from a pinned staging buffer (upload; kernel arguments under graph
+// capture), or kernels that take it as by-value arguments
+// (load_table_by_kernel: no staging memory, for pm_muon_step_noalloc).
 enum class TablePath { kStaged, kKernelArgs };
-int load_table_by_kernel(const char* src, size_t bytes, char* dst, hipStream_t stream);
 
 int run_group(Item* items, int count, int group, const pm_hparams* hp, int mode, const float* lr_dev,
               double lr_host, char* ws, hipStream_t stream, TablePath path) {
