@@ -410,8 +410,14 @@ __device__ __forceinline__ void gemm_unit(const Ring& ring, int u, const Engine&
       bf[1][p] = frag_b<TR>(e, cb, p, 1);
     }
     if (REL >= 1 && p >= 12) bf[0][p - 12] = frag_b<TR>(e, nb, p - 12, 0);
+    // odd positions walk the B fragments backwards, so consecutive MFMAs
+    // never change both operands (the B fragment is kept across a position
+    // change)
 #pragma unroll
-    for (int ni = 0; ni < kNi; ++ni) mfma16(acc[mi][ni], af[p % 8], bf[s][ni]);
+    for (int i = 0; i < kNi; ++i) {
+      const int ni = (p & 1) ? kNi - 1 - i : i;
+      mfma16(acc[mi][ni], af[p % 8], bf[s][ni]);
+    }
     if (e.copier) {  // waves 0..3: two copies per position
       if (REL >= 1 && p < 2) {
         dma_a(e, ring.a[S ^ 1], u + 1, 4 + 2 * p);
