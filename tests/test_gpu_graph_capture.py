@@ -121,3 +121,42 @@ def test_adam_step_captured_replays_the_eager_step():
             for i in range(len(sizes)):
                 assert torch.equal(got[k][i], ref[k][i]), f"list {k} tensor {i} after replay {rep}"
     graph.reset()
+
+
+def test_standalone_ops_captured_match_eager():
+    """pm_gram and pm_gemm_symmetric (descriptor tables as kernel arguments
+    under capture), pm_momentum_nesterov and pm_step_param (no table)."""
+    g = torch.Generator("cpu").manual_seed(830)
+    x = torch.randn(512, 768, generator=g).to(DEV, torch.bfloat16)
+    a, b, d = (torch.randn(512, 512, generator=g).to(DEV, torch.bfloat16) for _ in range(3))
+    buf0 = (torch.randn(300, 700, generator=g) * 1e-3).to(DEV)
+    grad = (torch.randn(300, 700, generator=g) * 1e-3).to(DEV, torch.bfloat16)
+    p0 = (torch.randn(300, 700, generator=g) * 0.02).to(DEV)
+    lr = torch.tensor(0.02, device=DEV)
+
+    def ops(buf, p):
+        r = _lib.gram(x)
+        s = _lib.gemm_symmetric(a, b, d, alpha=2.0, beta=-0.5)
+        u = torch.empty_like(grad)
+        _lib.momentum_nesterov_into(buf, grad, u, 0.95)
+        _lib.step_param_inplace(p, u, lr, 0.01, 1.5)
+        return r, s, u
+
+    want = ops(buf0.clone(), p0.clone())  # outside capture
+    torch.cuda.synchronize()
+    buf, p = buf0.clone(), p0.clone()
+    graph = torch.cuda.CUDAGraph()
+    print("standalone ops graph capture", flush=True)
+    with torch.cuda.graph(graph):
+        assert torch.cuda.is_current_stream_capturing()
+        got = ops(buf, p)
+    _lib.gram(x[:256, :256].contiguous())  # an eager call through the staging buffers
+    graph.replay()
+    torch.cuda.synchronize()
+    for i, (u, v) in enumerate(zip(got, want)):
+        assert torch.equal(u, v), f"output {i}"
+    ref_buf, ref_p = buf0.clone(), p0.clone()
+    ops(ref_buf, ref_p)
+    torch.cuda.synchronize()
+    assert torch.equal(buf, ref_buf) and torch.equal(p, ref_p)
+    graph.reset()
