@@ -849,20 +849,8 @@ __global__ __launch_bounds__(kGemmThreads, 4) void pm_small_prologue_kernel(ProA
   sm_gram_store(d.S[so], SmMat{units[0], units[1]}, acc, r0, c0, lane, inv * inv);
 }
 
-// A unit of X in LDS, laid out as in HBM (sm_x_off): kSm rows (k) of 64
-// columns (n), 128 B each. Chunk c (16 B, columns 8c .. 8c+7) of row k is
-// stored at chunk c ^ xt_swz(k). The LDS serves a 64-lane read 16 lanes at a
-// time, and the 16 lanes of a transposed fragment read (ds_read_b64_tr_b16)
-// address 4 consecutive rows k (4 columns of 8 bytes each), those of an a·X
-// quad read 4 consecutive rows too, and those of the wide FINAL's read 16
-// consecutive rows: with k bits 1, 3 and 1 ^ 2 in the XOR, each such group of
-// 16 lanes falls in distinct banks. (A XOR of k bits 3 and 4 alone put 2 or 4
-// lanes of a group on one bank: 53% of the apply's LDS cycles were bank
-// conflicts.)
-__device__ __forceinline__ int xt_swz(int k) {
-  return ((k >> 1) & 1) | (((k >> 3) & 1) << 1) | ((((k >> 1) ^ (k >> 2)) & 1) << 2);
-}
-__device__ __forceinline__ int xt_off(int k, int n) { return k * 128 + ((((n >> 3) & 7) ^ xt_swz(k)) << 4) + (n & 7) * 2; }
+// A unit of X in LDS is laid out by xt_off (pm_tiles.hpp): as in HBM
+// (sm_x_off), each row's 16-byte chunks permuted by xt_swz.
 
 // The MFMA B fragment of columns n0 .. n0+15 (n0 a multiple of 16) for k =
 // k0 .. k0+7 (k0 a multiple of 8) of a unit stored as xt_off lays it out:
@@ -1098,15 +1086,11 @@ __global__ __launch_bounds__(kSmApplyThreads, 1) void pm_small_apply_kernel(Gemm
   SmWalk kw = cw;
   int cu = u0;  // the unit the copy walk issues next
 
-  // lane offsets of this wave's X copies: copy q = kXCopies·w + h moves rows
-  // 8q .. 8q+7 of the unit; lane l lands at row k = 8q + l/8, stored chunk
-  // l%8, so it loads logical chunk (l%8) ^ xt_swz(k)
+  // lane offsets of this wave's X copies (copy q = kXCopies·w + h moves rows
+  // 8q .. 8q+7 of the unit)
   int xvo[C::kXCopies];
 #pragma unroll
-  for (int h = 0; h < C::kXCopies; ++h) {
-    const int k = 8 * (C::kXCopies * w + h) + (lane >> 3);
-    xvo[h] = k * 128 + (((lane & 7) ^ xt_swz(k)) << 4);
-  }
+  for (int h = 0; h < C::kXCopies; ++h) xvo[h] = xt_copy_src(C::kXCopies * w + h, lane);
 
   // Issues the copies of the copy walk's unit into slot S (zero-length
   // copies past the block's range, so every unit issues kCopies per wave),

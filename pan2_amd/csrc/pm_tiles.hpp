@@ -142,4 +142,23 @@ PM_HD int64_t ws_off(int r, int c, int64_t ld, bool tiled) {
 // unit c/64 is a contiguous 16 KiB block of 128 rows of 128 bytes.
 PM_HD int64_t sm_x_off(int r, int c) { return ((int64_t)(c >> 6) << 13) + (r << 6) + (c & 63); }
 
+// A unit of a small matrix's X in the apply's LDS ring: its 128 rows (k) of
+// 64 columns (n), 128 B each, chunk c (16 B, columns 8c .. 8c+7) of row k
+// stored at chunk c ^ xt_swz(k). The LDS serves a 64-lane read 16 lanes at a
+// time; the 16 lanes of a transposed fragment read (ds_read_b64_tr_b16)
+// address 4 consecutive rows, those of an a·X quad read 4 consecutive rows
+// too, and those of the wide FINAL's read 16 consecutive rows: with k bits
+// 1, 3 and 1 ^ 2 in the XOR each such group falls in distinct banks. (A XOR
+// of k bits 3 and 4 alone put 2 or 4 lanes of a group on one bank: 53% of
+// the apply's LDS cycles were bank conflicts.) Byte offset of (k, n):
+PM_HD int xt_swz(int k) { return ((k >> 1) & 1) | (((k >> 3) & 1) << 1) | ((((k >> 1) ^ (k >> 2)) & 1) << 2); }
+PM_HD int xt_off(int k, int n) { return k * 128 + ((((n >> 3) & 7) ^ xt_swz(k)) << 4) + (n & 7) * 2; }
+// The unit's copies into the ring: copy q (0..15) writes its 1 KiB in order,
+// lane l filling row k = 8q + l/8 at stored chunk l%8, so it reads the
+// unit's (row-major, 128 B a row) bytes at this offset.
+PM_HD int xt_copy_src(int q, int lane) {
+  const int k = 8 * q + (lane >> 3);
+  return k * 128 + (((lane & 7) ^ xt_swz(k)) << 4);
+}
+
 }  // namespace pm
