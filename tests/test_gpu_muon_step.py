@@ -17,6 +17,7 @@ import torch
 
 import torch.optim._muon as torch_muon
 from oracle import muon_ref
+from pan2_amd import _lib
 from pan2_amd.optim.muon import build_native_muon_optimizers
 from pan2_amd.optim.patch_muon import patch_muon
 from tests.test_gpu_full_size import band
@@ -223,3 +224,33 @@ def test_factory_tensor_lr_installs_hip_path():
         assert torch.isfinite(model[0].weight).all()
     finally:
         torch_muon._zeropower_via_newtonschulz, torch_muon._single_tensor_muon = saved
+
+
+def test_fused_step_without_nesterov_through_the_abi():
+    """pm_muon_step with nesterov = 0 (the header's u = buf; PAN 2's patch
+    asserts nesterov, so only the C ABI reaches it): the fused prologue's
+    momentum is bit-exact against the oracle, and the update is NS(buf)
+    within the fp64 gate, on engine, small and tall matrices."""
+    shapes = [(512, 1024), (700, 300), (96, 2000)]
+    lr = 0.02
+    g = torch.Generator("cpu").manual_seed(77)
+    init = [((torch.randn(*s, generator=g) * 0.02).numpy(), (torch.randn(*s, generator=g) * 1e-3).numpy(),
+             (torch.randn(*s, generator=g) * 1e-3).numpy()) for s in shapes]
+    ps = [torch.from_numpy(p).to(DEV) for p, _, _ in init]
+    gs = [torch.from_numpy(gr).to(DEV) for _, gr, _ in init]
+    bs = [torch.from_numpy(b).to(DEV) for _, _, b in init]
+    ratios = [muon_ref.adjust_lr_ratio(None, s) for s in shapes]
+    print(f"non-nesterov fused step {shapes}", flush=True)
+    _lib.muon_step(ps, gs, bs, ratios, lr=lr, weight_decay=0.01, momentum=0.95, nesterov=False,
+                   ns_coefficients=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7)
+    torch.cuda.synchronize()
+    for p, b, (p0, g0, b0), s, r in zip(ps, bs, init, shapes, ratios):
+        _, ref_b, ref_o = muon_ref.muon_step(p0, g0, b0, lr=lr, weight_decay=0.01, nesterov=False,
+                                             ns_precision="fp64")
+        assert np.array_equal(b.cpu().numpy(), ref_b), s
+        o_got = (p0.astype(np.float64) * (1 - lr * 0.01) - p.cpu().numpy()) / (lr * r)
+        err = float(np.linalg.norm(o_got - ref_o) / np.linalg.norm(ref_o))
+        assert err <= 2e-2, (s, err)
+        # and it is NS of the momentum buffer, not of the Nesterov blend
+        ref_o_nest = muon_ref.muon_step(p0, g0, b0, lr=lr, weight_decay=0.01, ns_precision="fp64")[2]
+        assert np.linalg.norm(o_got - ref_o_nest) > np.linalg.norm(o_got - ref_o), s
